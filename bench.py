@@ -1,0 +1,235 @@
+"""Benchmark: milliseconds of DiT + SAME-L differential attention per 120 s clip on one MI355X.
+
+One step is one clip's worth of the hot path with inputs resident in HBM:
+  192 dense calls  (8 sampler steps x 24 DiT blocks), B=2 (CFG), L=2584 tokens, 24 heads x 64, bf16
+  + 12 band calls (12 SAME-L decoder blocks), B=1, S=82688 frames, 8 heads x 64, half-width w=128, bf16
+Each call is the full C-ABI operation (dense: prep + attention kernels; band: one kernel) on preallocated
+buffers. Inputs follow the seeded recipe of `hummingbird_amd.workloads` (synthetic data, random gains).
+
+The JSON line also carries, for the dominant kernel (dense attention), a roofline object computed from its
+average launch duration measured here with HIP events on its own stream, and the same for the band kernel
+(`roofline_band`); plus the CPU baseline: the NumPy restatement of the reference XLA chains (the oracle, fp32
+accumulation) timed on a bounded sample on this host and scaled to one clip.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--kernel-iters", type=int, default=50, help="launches per live kernel timing")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    return ap.parse_args()
+
+
+def cpu_baseline(target_s: float) -> dict:
+    """Time the oracle (NumPy restatement of the reference XLA chains, fp32 accumulation) on a bounded sample
+    of the clip's work and scale it to ms per clip."""
+    from threadpoolctl import threadpool_info
+
+    from hummingbird_amd import workloads as wl
+    from oracle import band as oband
+    from oracle import dense as odense
+
+    d, b = wl.DENSE_120S, wl.BAND_120S
+    # dense: one full-length (batch, head) pair at a time
+    inp = wl.dense_inputs(1, d["length"], 1, d["head_dim"], seed=0, dtype="fp32")
+    args = (inp["qkv"], inp["q_weight"], inp["k_weight"], inp["inv_freq"], inp["valid"], 1, d["head_dim"], 1e-6,
+            inp["lam"], "fp32", np.float32)
+    odense.dense_xla(*args)  # warm
+    t0 = time.perf_counter()
+    n_dense = 0
+    while time.perf_counter() - t0 < target_s / 2 or n_dense < 2:
+        odense.dense_xla(*args)
+        n_dense += 1
+    dense_head_s = (time.perf_counter() - t0) / n_dense
+    dense_call_s = dense_head_s * d["batch"] * d["heads"]
+    # band: one head over a 16384-frame slice of the sequence
+    frames = 16384
+    binp = wl.band_inputs(1, frames, 1, b["head_dim"], b["window"], seed=1, dtype="fp32")
+    bargs = (binp["qkv"], binp["q_norm"], binp["k_norm"], binp["inv_freq"], 1, b["head_dim"], b["window"], binp["lam"],
+             "fp32", np.float32)
+    oband.band_xla(*bargs)
+    t0 = time.perf_counter()
+    n_band = 0
+    while time.perf_counter() - t0 < target_s / 2 or n_band < 2:
+        oband.band_xla(*bargs)
+        n_band += 1
+    band_slice_s = (time.perf_counter() - t0) / n_band
+    band_call_s = band_slice_s * (b["length"] / frames) * b["batch"] * b["heads"]
+    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    ms_clip = 1e3 * (wl.DENSE_CALLS_PER_CLIP * dense_call_s + wl.BAND_CALLS_PER_CLIP * band_call_s)
+    return {"value": round(ms_clip, 1), "unit": "ms/120s-clip", "cores": int(threads), "kind": "port",
+            "sample": (f"oracle (NumPy fp32 XLA-chain restatement): dense 1 of {d['batch'] * d['heads']} (batch, head) "
+                       f"pairs at L={d['length']} x{n_dense}, {dense_call_s * 1e3:.0f} ms/call scaled; band 1 of "
+                       f"{b['heads']} heads over {frames} of {b['length']} frames x{n_band}, "
+                       f"{band_call_s * 1e3:.0f} ms/call scaled; host cpus={len(os.sched_getaffinity(0))}")}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 (the kernels shard by "
+                                   "(batch, head) and by sequence with a halo, which is described but not built)"}))
+        return 2
+
+    import torch
+
+    from hummingbird_amd import _lib
+    from hummingbird_amd import band_attention as ba
+    from hummingbird_amd import dense_attention as da
+    from hummingbird_amd import workloads as wl
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+
+    # ---- dense inputs (two qkv buffers alternate, as consecutive blocks would) ----
+    d = wl.DENSE_120S
+    B, L, H, D = d["batch"], d["length"], d["heads"], d["head_dim"]
+    dinp = wl.dense_inputs(B, L, H, D, seed=0)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    qkv_d = [torch.from_numpy(dinp["qkv"]).to(dev, torch.bfloat16),
+             torch.randn((B, L, 5 * H * D), device=dev, generator=gen).to(torch.bfloat16)]
+    qw = torch.from_numpy(dinp["q_weight"]).to(dev)
+    kw = torch.from_numpy(dinp["k_weight"]).to(dev)
+    lam_d = torch.from_numpy(dinp["lam"]).to(dev)
+    cos_d, sin_d, mask_d = da.tables(L, torch.from_numpy(dinp["inv_freq"]).to(dev),
+                                     torch.from_numpy(dinp["valid"]).to(dev), D, torch.bfloat16)
+    half_d = dinp["half"]
+    ws_bytes = int(lib.hb_dense_workspace_size(_lib.HB_BF16, B, L, H, D))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out_d = torch.empty((B, L, H * D), dtype=torch.bfloat16, device=dev)
+
+    # ---- band inputs ----
+    bcfg = wl.BAND_120S
+    S, HB, DB, W = bcfg["length"], bcfg["heads"], bcfg["head_dim"], bcfg["window"]
+    binp = wl.band_inputs(1, S, HB, DB, W, seed=1)
+    qkv_b = torch.from_numpy(binp["qkv"]).to(dev, torch.bfloat16)
+    qdyt = ba.pack_dyt({k: torch.as_tensor(np.asarray(v)) for k, v in binp["q_norm"].items()}, DB, dev)
+    kdyt = ba.pack_dyt({k: torch.as_tensor(np.asarray(v)) for k, v in binp["k_norm"].items()}, DB, dev)
+    cos_b, sin_b = ba.rope_tables(S, torch.from_numpy(binp["inv_freq"]).to(dev))
+    lam_b = torch.from_numpy(binp["lam"]).to(dev)
+    out_b = torch.empty((1, S, HB * DB), dtype=torch.bfloat16, device=dev)
+    half_b = binp["half"]
+    del dinp, binp
+
+    def dense_call(i: int) -> None:
+        q = qkv_d[i & 1]
+        _lib.check(lib.hb_dense_diffattn(sp, q.data_ptr(), _lib.HB_BF16, 5 * H * D, qw.data_ptr(), kw.data_ptr(),
+                                         cos_d.data_ptr(), sin_d.data_ptr(), half_d, mask_d.data_ptr(),
+                                         lam_d.data_ptr(), out_d.data_ptr(), B, L, H, D, 1e-6, ws.data_ptr(),
+                                         ws_bytes), "dense")
+
+    def band_call() -> None:
+        _lib.check(lib.hb_band_diffattn(sp, qkv_b.data_ptr(), _lib.HB_BF16, 5 * HB * DB, qdyt.data_ptr(),
+                                        kdyt.data_ptr(), cos_b.data_ptr(), sin_b.data_ptr(), half_b, W,
+                                        lam_b.data_ptr(), out_b.data_ptr(), 1, S, HB, DB), "band")
+
+    def step() -> None:
+        for i in range(wl.DENSE_CALLS_PER_CLIP):
+            dense_call(i)
+        for _ in range(wl.BAND_CALLS_PER_CLIP):
+            band_call()
+
+    print(f"[bench] warmup {args.warmup} clip(s)", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    print(f"[bench] timing {args.steps} clip(s)", file=sys.stderr, flush=True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_host = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    host_s = time.perf_counter() - t_host
+    ms_clip = start.elapsed_time(stop) / args.steps
+
+    # ---- live per-kernel timing (HIP events on the launch stream) ----
+    def timed(fn, n: int) -> float:
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(n):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n * 1e-3  # seconds per launch
+
+    dense_call(0)  # workspace now holds prepared q/k/v for the attention-only timing
+    attend_s = timed(lambda: _lib.check(lib.hb_dense_attend(sp, ws.data_ptr(), ws_bytes, _lib.HB_BF16, qw.data_ptr(),
+                                                            kw.data_ptr(), lam_d.data_ptr(), out_d.data_ptr(), B, L,
+                                                            H, D), "attend"), args.kernel_iters)
+    prep_s = timed(lambda: _lib.check(lib.hb_dense_prep(sp, qkv_d[0].data_ptr(), _lib.HB_BF16, 5 * H * D,
+                                                        qw.data_ptr(), kw.data_ptr(), cos_d.data_ptr(),
+                                                        sin_d.data_ptr(), half_d, mask_d.data_ptr(), B, L, H, D, 1e-6,
+                                                        ws.data_ptr(), ws_bytes), "prep"), args.kernel_iters)
+    band_s = timed(band_call, max(5, args.kernel_iters // 5))
+    dense_fl, dense_by = wl.dense_flops(B, L, H, D), wl.dense_bytes(B, L, H, D)
+    band_fl, band_by = wl.band_flops(1, S, HB, DB, W), wl.band_bytes(1, S, HB, DB)
+    attend_tf = dense_fl / attend_s / 1e12
+    band_gbs = band_by / band_s / 1e9
+
+    result = {
+        "metric": "ms/120s-clip for DiT+SAME-L attention; % bf16 MFMA peak and % HBM GB/s",
+        "value": round(ms_clip, 3),
+        "unit": "ms/120s-clip",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_clip, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) qkv, random gains; hummingbird_amd.workloads)",
+        "config": {"workload": "120 s clip: 192 x DiT dense diff-attn (B=2, L=2584, H=24, D=64) + 12 x SAME-L "
+                               "band diff-attn (B=1, S=82688, H=8, D=64, w=128)",
+                   "dense_ms_per_call": round((attend_s + prep_s) * 1e3, 4),
+                   "band_ms_per_call": round(band_s * 1e3, 4),
+                   "host_wall_s": round(host_s, 3)},
+        "roofline": {"bound": "mfma", "achieved": round(attend_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(attend_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "dense_attend_bf16<64>", "avg_us": round(attend_s * 1e6, 2),
+                     "flops_per_launch": dense_fl},
+        "roofline_band": {"bound": "hbm", "achieved": round(band_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(band_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                          "kernel": "band_attend_bf16<64>", "avg_us": round(band_s * 1e6, 2),
+                          "bytes_per_launch": band_by, "tflops": round(band_fl / band_s / 1e12, 1)},
+        # prep reads the 5 qkv sections and writes them back prepared: 2 x 5 H D bf16 per token
+        "dense_prep": {"avg_us": round(prep_s * 1e6, 2), "gbs": round(2 * B * L * 5 * H * D * 2 / prep_s / 1e9, 1)},
+    }
+    if not args.no_cpu:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,100 @@
+"""SAME-L band differential attention on MI355X: the `attention="hip"` counterpart of the reference's
+`sa3jax/band_attention.py` (same function names, argument meaning and error behaviour).
+
+`band_attention` runs DyT -> RoPE -> both windowed softmax branches -> subtract on the GPU through the C ABI
+(`hb_band_diffattn`), replacing the Pallas kernel (band_attention.py:123-180). `rope_tables` replaces the
+reference's lane tables (band_attention.py:43-58) with `(length, half)` fp32 tables built on the device.
+"""
+from __future__ import annotations
+
+import weakref
+
+import torch
+
+from hummingbird_amd import _lib
+from hummingbird_amd.dense_attention import (SUPPORTED_HEAD_DIMS, _f32, _require_gpu, _row_stride, dtype_code,
+                                             rope_tables)
+
+__all__ = ["band_attention", "rope_tables", "pack_dyt"]
+
+# RoPE tables keyed by the identity and version of the inv_freq tensor (in-place edits bump the version), so a
+# decoder's repeated calls with the same buffer reuse one table instead of rebuilding it per call.
+_TABLE_CACHE: dict = {}
+
+
+def _cached_tables(inv_freq: torch.Tensor, length: int) -> tuple[torch.Tensor, torch.Tensor]:
+    key = (id(inv_freq), inv_freq._version, length, inv_freq.device)
+    hit = _TABLE_CACHE.get(key)
+    if hit is not None and hit[0]() is inv_freq:
+        return hit[1], hit[2]
+    cos, sin = rope_tables(length, inv_freq)
+    if len(_TABLE_CACHE) > 64:
+        _TABLE_CACHE.clear()
+    _TABLE_CACHE[key] = (weakref.ref(inv_freq), cos, sin)
+    return cos, sin
+
+
+def pack_dyt(norm: dict, head_dim: int, device: torch.device) -> torch.Tensor:
+    """`{alpha: scalar, gamma: (D,), beta: (D,)}` (the DyT params of sa3jax/same_l.py:58-69) -> the C ABI's
+    `[alpha, gamma[0..D), beta[0..D)]` fp32 vector."""
+    alpha = torch.as_tensor(norm["alpha"]).to(device=device, dtype=torch.float32).reshape(-1)
+    gamma = torch.as_tensor(norm["gamma"]).to(device=device, dtype=torch.float32).reshape(-1)
+    beta = torch.as_tensor(norm["beta"]).to(device=device, dtype=torch.float32).reshape(-1)
+    if alpha.numel() != 1 or gamma.numel() != head_dim or beta.numel() != head_dim:
+        raise ValueError(f"DyT params need a scalar alpha and (head_dim={head_dim},) gamma and beta")
+    return torch.cat([alpha, gamma, beta]).contiguous()
+
+
+def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torch.Tensor, num_heads: int,
+                   head_dim: int, window: int, *, rows: int = 1024, halo: int = 32, sub: int = 256,
+                   stack: bool = True, interpret: bool = False, lam: torch.Tensor | None = None,
+                   tables: tuple[torch.Tensor, torch.Tensor] | None = None) -> torch.Tensor:
+    """`(B, S, 5 * H * D)` projection output -> `(B, S, H * D)` differential band attention, in `qkv.dtype`.
+
+    Same contract as the reference (sa3jax/band_attention.py:123-135): `q_norm`/`k_norm` are the block's DyT
+    params (`alpha` scalar, `gamma`/`beta` `(D,)`), shared by both branches; a query at position p sees keys
+    `|k - p| <= window` inside `[0, S)`. `rows`, `halo`, `sub`, `stack` and `interpret` are the TPU kernel's
+    tiling knobs and are accepted and ignored (the reference's `halo >= window` constraint does not apply: the
+    HIP kernel takes any window >= 0). `lam` `(H,)` optionally weights the second branch (default 1, the
+    reference). `tables` optionally supplies `(cos, sin)` from `rope_tables(S, inv_freq)`.
+    """
+    del rows, halo, sub, stack, interpret
+    _require_gpu(qkv, "qkv")
+    if qkv.dim() != 3:
+        raise ValueError(f"qkv must be (B, S, 5*H*D), got shape {tuple(qkv.shape)}")
+    if head_dim not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"band_attention needs head_dim in {SUPPORTED_HEAD_DIMS} (head_dim={head_dim})")
+    if window < 0:
+        raise ValueError(f"band_attention needs window >= 0 (window={window})")
+    batch, length, width = qkv.shape
+    if width != 5 * num_heads * head_dim:
+        raise ValueError(f"qkv width {width} != 5 * num_heads * head_dim = {5 * num_heads * head_dim}")
+    dev = qkv.device
+    half = inv_freq.shape[0]
+    if not 0 <= half <= head_dim // 2:
+        raise ValueError(f"inv_freq has {half} entries; the rotary half-width must be in [0, head_dim/2]")
+    code = dtype_code(qkv.dtype)
+    rs = _row_stride(qkv)
+    qd, kd = pack_dyt(q_norm, head_dim, dev), pack_dyt(k_norm, head_dim, dev)
+    cos_p = sin_p = 0
+    if half > 0:
+        if tables is None:
+            cos, sin = _cached_tables(inv_freq.to(dev) if inv_freq.device != dev else inv_freq, length)
+        else:
+            cos, sin = (_f32(t, dev) for t in tables)
+            if tuple(cos.shape) != (length, half) or tuple(sin.shape) != (length, half):
+                raise ValueError(f"tables must be (S, half) = ({length}, {half})")
+        cos_p, sin_p = cos.data_ptr(), sin.data_ptr()
+    lam_p = 0
+    if lam is not None:
+        lam = _f32(lam, dev).reshape(-1)
+        if lam.numel() != num_heads:
+            raise ValueError("lam must have num_heads elements")
+        lam_p = lam.data_ptr()
+    out = torch.empty((batch, length, num_heads * head_dim), dtype=qkv.dtype, device=dev)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    status = lib.hb_band_diffattn(stream, qkv.data_ptr(), code, rs, qd.data_ptr(), kd.data_ptr(), cos_p, sin_p, half,
+                                  int(window), lam_p, out.data_ptr(), batch, length, num_heads, head_dim)
+    _lib.check(status, "band_attention")
+    return out

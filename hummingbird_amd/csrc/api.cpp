@@ -1,0 +1,95 @@
+// Status reporting and argument validation for the C ABI (host code only; no kernels here).
+#include "api.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace hb {
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+void clear_error() { g_last_error[0] = '\0'; }
+
+DenseLayout dense_layout(int dtype, int B, int L, int H, int D) {
+  DenseLayout lay;
+  lay.Lp = round_up(L, kDenseQueryBlock);
+  lay.region_elems = static_cast<int64_t>(B) * H * lay.Lp * D;
+  lay.elem_bytes = dtype == HB_F32 ? 4 : 2;
+  lay.region_bytes = static_cast<size_t>(lay.region_elems) * lay.elem_bytes;
+  lay.total_bytes = 5 * lay.region_bytes;
+  return lay;
+}
+
+int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int half) {
+  if (dtype != HB_BF16 && dtype != HB_F32) return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0) or HB_F32 (1)", dtype);
+  if (D != 64 && D != 128) return fail(HB_ERR_HEAD_DIM, "head_dim %d is not 64 or 128", D);
+  if (B < 1 || N < 1 || H < 1) return fail(HB_ERR_SHAPE, "need B, N, H >= 1 (B=%d, N=%d, H=%d)", B, N, H);
+  if (B > 65535 || H > 65535 || N > (1 << 28))
+    return fail(HB_ERR_SHAPE, "shape out of range (B=%d <= 65535, H=%d <= 65535, N=%d <= 2^28)", B, H, N);
+  if (static_cast<int64_t>(B) * N * H * D > (int64_t(1) << 40))
+    return fail(HB_ERR_SHAPE, "B*N*H*D exceeds 2^40 elements");
+  if (half < 0 || 2 * half > D) return fail(HB_ERR_HALF, "half %d outside [0, D/2=%d]", half, D / 2);
+  if (row_stride < static_cast<int64_t>(5) * H * D || row_stride % 8 != 0)
+    return fail(HB_ERR_STRIDE, "row_stride %lld must be >= 5*H*D=%lld and a multiple of 8",
+                static_cast<long long>(row_stride), static_cast<long long>(5) * H * D);
+  return HB_OK;
+}
+
+}  // namespace hb
+
+extern "C" {
+
+const char* hb_last_error(void) { return hb::g_last_error; }
+
+const char* hb_version(void) { return "hummingbird_amd 0.1.0 (gfx950)"; }
+
+const char* hb_status_name(int status) {
+  switch (status) {
+    case HB_OK: return "HB_OK";
+    case HB_ERR_NULL: return "HB_ERR_NULL";
+    case HB_ERR_SHAPE: return "HB_ERR_SHAPE";
+    case HB_ERR_DTYPE: return "HB_ERR_DTYPE";
+    case HB_ERR_HEAD_DIM: return "HB_ERR_HEAD_DIM";
+    case HB_ERR_HALF: return "HB_ERR_HALF";
+    case HB_ERR_WINDOW: return "HB_ERR_WINDOW";
+    case HB_ERR_STRIDE: return "HB_ERR_STRIDE";
+    case HB_ERR_WORKSPACE: return "HB_ERR_WORKSPACE";
+    case HB_ERR_LAUNCH: return "HB_ERR_LAUNCH";
+    case HB_ERR_EPS: return "HB_ERR_EPS";
+    default: return "HB_ERR_UNKNOWN";
+  }
+}
+
+size_t hb_dense_workspace_size(int dtype, int B, int L, int H, int D) {
+  if ((dtype != HB_BF16 && dtype != HB_F32) || B < 1 || L < 1 || H < 1 || (D != 64 && D != 128)) return 0;
+  return hb::dense_layout(dtype, B, L, H, D).total_bytes;
+}
+
+int hb_dense_validate(int dtype, int64_t row_stride, int B, int L, int H, int D, int half, float eps) {
+  hb::clear_error();
+  int st = hb::check_common(dtype, row_stride, B, L, H, D, half);
+  if (st) return st;
+  if (!(eps >= 0.0f) || !isfinite(eps)) return hb::fail(HB_ERR_EPS, "eps %g must be finite and >= 0", eps);
+  return HB_OK;
+}
+
+int hb_band_validate(int dtype, int64_t row_stride, int B, int S, int H, int D, int half, int window) {
+  hb::clear_error();
+  int st = hb::check_common(dtype, row_stride, B, S, H, D, half);
+  if (st) return st;
+  if (window < 0) return hb::fail(HB_ERR_WINDOW, "window %d must be >= 0", window);
+  return HB_OK;
+}
+
+}  // extern "C"

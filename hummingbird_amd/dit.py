@@ -1,0 +1,57 @@
+"""The DiT self-attention call site with the `attention="hip"` dispatch (sa3jax/dit.py:179-200) and the
+per-clip table preparation it reads (sa3jax/dit.py:317-336).
+
+Only the attention step of a DiT block is here: `to_qkv` -> differential self-attention -> `to_out`. The
+rest of the block (adaLN, cross-attention, feed-forward) is outside this package.
+"""
+from __future__ import annotations
+
+import torch
+
+from hummingbird_amd import dense_attention, xla_chain
+from hummingbird_amd.config import DiTConfig
+
+
+def use_hip(cfg: DiTConfig, qkv: torch.Tensor) -> bool:
+    """Dispatch predicate (reference: dit._fused, dit.py:179-182): the HIP kernel when selected, the model is
+    differential and the tensors live on a ROCm device. There is no token floor. Selecting "hip" for CPU
+    tensors is an error rather than a silent fallback."""
+    if cfg.attention != "hip" or not cfg.differential:
+        return False
+    if not qkv.is_cuda:
+        raise ValueError('attention="hip" needs ROCm device tensors; use attention="xla" on the CPU')
+    return True
+
+
+def static_tables(inv_freq: torch.Tensor, valid: torch.Tensor, cfg: DiTConfig,
+                  compute: torch.dtype) -> dict[str, torch.Tensor]:
+    """Per-clip tables (reference: dit._static, dit.py:317-336). `valid` is the `(B, T)` padding mask of the
+    latents; the mask is extended over the memory tokens (dit.py:320)."""
+    batch = valid.shape[0]
+    ones = torch.ones((batch, cfg.num_memory_tokens), dtype=torch.bool, device=valid.device)
+    full = torch.cat([ones, valid.to(torch.bool)], dim=-1)
+    length = full.shape[1]
+    static = {"inv_freq": inv_freq, "valid": full}
+    if cfg.attention == "hip":
+        static["hip_cos"], static["hip_sin"], static["hip_mask"] = dense_attention.tables(
+            length, inv_freq, full, cfg.head_dim, compute)
+    return static
+
+
+def self_attention(h: torch.Tensor, block: dict, static: dict, cfg: DiTConfig,
+                   lam: torch.Tensor | None = None) -> torch.Tensor:
+    """`to_qkv` -> differential self-attention -> `to_out` (reference: dit._self_attention, dit.py:185-200).
+    `block["self_attn"]` holds `to_qkv.weight (5E, E)`, `to_out.weight (E, E)`, `q_norm.weight`, `k_norm.weight`."""
+    attn = block["self_attn"]
+    qkv = h @ attn["to_qkv"]["weight"].t()
+    if use_hip(cfg, qkv):
+        out = dense_attention.dense_attention(qkv, attn["q_norm"]["weight"], attn["k_norm"]["weight"],
+                                              static["hip_cos"], static["hip_sin"], static["hip_mask"],
+                                              cfg.num_heads, cfg.head_dim, cfg.rope_dim // 2, cfg.qk_norm_eps,
+                                              lam=lam)
+    else:
+        if not cfg.differential:
+            raise NotImplementedError("only the differential self-attention is on this package's path")
+        out = xla_chain.dense_chain(qkv, attn["q_norm"]["weight"], attn["k_norm"]["weight"], static["inv_freq"],
+                                    static["valid"], cfg.num_heads, cfg.head_dim, cfg.qk_norm_eps, lam=lam)
+    return out @ attn["to_out"]["weight"].t()

@@ -1,0 +1,119 @@
+/* hummingbird_amd: MI355X (gfx950) differential-attention kernels behind a plain C ABI.
+ *
+ * Two operations replace the reference's two fused TPU kernels (kelechi-c/hummingbird, sa3jax/):
+ *
+ *   hb_dense_diffattn  replaces  dense_attention.dense_attention  (sa3jax/dense_attention.py:104-153),
+ *                      called from dit._self_attention (sa3jax/dit.py:191-195);
+ *   hb_band_diffattn   replaces  band_attention.band_attention    (sa3jax/band_attention.py:123-180),
+ *                      called from same_l._attention (sa3jax/same_l.py:158-161);
+ *   hb_rope_tables     replaces  band_attention.rope_tables / dit._rope_tables
+ *                      (sa3jax/band_attention.py:43-58, sa3jax/dit.py:82-87) in a kernel-native layout.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers except where stated. Nothing is allocated: scratch is the caller's
+ *     `workspace` (size from hb_dense_workspace_size).
+ *   - Work is enqueued on `stream`; no entry point synchronises the host.
+ *   - The packed input `qkv` is (B, N, 5*H*D) = [q | k | v | q_diff | k_diff], head-major inside each section
+ *     (sa3jax/dit.py:196-198, sa3jax/same_l.py:162). Element (b, n, c) sits at
+ *     qkv[(b*N + n) * row_stride + c]; row_stride >= 5*H*D and a multiple of 8 elements; qkv 16-byte aligned.
+ *   - The output `out` is dense (B, N, H*D) in `b n (h d)` order (sa3jax/dit.py:107-110), dtype = input dtype.
+ *   - `lam` (H floats, or NULL for all ones) weights the second branch: out = A - lam[h] * B. lam = 1 is the
+ *     reference's unweighted difference (sa3jax/dit.py:146, sa3jax/same_l.py:168).
+ *   - Return value: HB_OK, or an HB_ERR_* code; hb_last_error() then describes the failure (thread-local).
+ *     Shape errors correspond to the reference's trace-time ValueErrors (sa3jax/dense_attention.py:119-120,
+ *     sa3jax/band_attention.py:138-140).
+ */
+#ifndef HUMMINGBIRD_AMD_H
+#define HUMMINGBIRD_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum hb_status {
+  HB_OK = 0,
+  HB_ERR_NULL = 1,      /* a required pointer is NULL */
+  HB_ERR_SHAPE = 2,     /* B, N or H out of range */
+  HB_ERR_DTYPE = 3,     /* dtype is not HB_BF16 or HB_F32 */
+  HB_ERR_HEAD_DIM = 4,  /* D is not 64 or 128 */
+  HB_ERR_HALF = 5,      /* rotary half-width outside [0, D/2] */
+  HB_ERR_WINDOW = 6,    /* band half-width < 0 */
+  HB_ERR_STRIDE = 7,    /* row_stride < 5*H*D, not a multiple of 8, or qkv misaligned */
+  HB_ERR_WORKSPACE = 8, /* workspace missing, too small or misaligned */
+  HB_ERR_LAUNCH = 9,    /* the HIP runtime rejected a launch */
+  HB_ERR_EPS = 10       /* eps < 0 or not finite */
+};
+
+enum hb_dtype { HB_BF16 = 0, HB_F32 = 1 };
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* hb_last_error(void);
+/* Static name of a status code. */
+const char* hb_status_name(int status);
+/* Library version string. */
+const char* hb_version(void);
+
+/* ---- RoPE tables ---------------------------------------------------------------------------------------
+ * cos[n*half + j] = cos(fp32(n) * inv_freq[j]), sin likewise, for n in [0, length), j in [0, half).
+ * The angle is the fp32 product, as in the reference (sa3jax/dit.py:85, sa3jax/same_l.py:87); its cosine and
+ * sine are evaluated in double precision and rounded once. These (length, half) tables hold the same values
+ * as the reference's duplicated (length, 2*half) tables and its lane tables (sa3jax/band_attention.py:49-58). */
+int hb_rope_tables(hipStream_t stream, const float* inv_freq, int half, int length, float* cos, float* sin);
+
+/* ---- DiT dense differential self-attention --------------------------------------------------------------
+ * Replaces dense_attention.dense_attention (sa3jax/dense_attention.py:104-153) and the XLA chain it stands
+ * in for (sa3jax/dit.py:185-200). Per (batch b, head h), with `x` the head's D-slice of a section:
+ *   q, q_diff <- RoPE(RMSNorm(x; q_weight, eps)),   k, k_diff <- RoPE(RMSNorm(x; k_weight, eps)),
+ *   v <- v * vmask[b, n],
+ *   out = softmax(q k^T / sqrt(D)) v - lam[h] * softmax(q_diff k_diff^T / sqrt(D)) v,
+ * with RMSNorm as sa3jax/dit.py:45-57 and half-half rotate_half RoPE over the first 2*half dims as
+ * sa3jax/dit.py:90-98. The softmax sees every key; vmask zeroes values only (sa3jax/dit.py:113-116).
+ *   q_weight, k_weight : D floats (RMSNorm scales)
+ *   cos, sin           : (L, half) floats from hb_rope_tables (ignored when half == 0)
+ *   vmask              : (B, L) floats, or NULL for all ones
+ *   dtype              : HB_BF16 or HB_F32 (of qkv and out)
+ *   D                  : 64 or 128;  0 <= half <= D/2;  eps >= 0
+ *   workspace          : >= hb_dense_workspace_size(dtype, B, L, H, D) bytes, 256-byte aligned; holds the
+ *                        prepared q/k/v for the duration of the call (stream-ordered).
+ * Internally two kernels run on `stream`: hb_dense_prep then hb_dense_attend (exported separately below). */
+size_t hb_dense_workspace_size(int dtype, int B, int L, int H, int D);
+int hb_dense_validate(int dtype, int64_t row_stride, int B, int L, int H, int D, int half, float eps);
+int hb_dense_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
+                      const float* q_weight, const float* k_weight, const float* cos, const float* sin, int half,
+                      const float* vmask, const float* lam, void* out, int B, int L, int H, int D, float eps,
+                      void* workspace, size_t workspace_bytes);
+/* Stage 1: RMSNorm + RoPE of q, k, q_diff, k_diff and V-masking into `workspace` (kernel-native layout). */
+int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
+                  const float* q_weight, const float* k_weight, const float* cos, const float* sin, int half,
+                  const float* vmask, int B, int L, int H, int D, float eps, void* workspace,
+                  size_t workspace_bytes);
+/* Stage 2: both softmax attentions and the subtraction from a workspace filled by hb_dense_prep. */
+int hb_dense_attend(hipStream_t stream, const void* workspace, size_t workspace_bytes, int dtype,
+                    const float* q_weight, const float* k_weight, const float* lam, void* out,
+                    int B, int L, int H, int D);
+
+/* ---- SAME-L band differential attention -----------------------------------------------------------------
+ * Replaces band_attention.band_attention (sa3jax/band_attention.py:123-180) and the XLA chain it stands in
+ * for (sa3jax/same_l.py:151-169). Per (batch b, head h):
+ *   q, q_diff <- RoPE(DyT(x; q_dyt)),   k, k_diff <- RoPE(DyT(x; k_dyt)),   DyT(x) = gamma*tanh(alpha*x)+beta,
+ *   out[i] = sum_{|j-i|<=window, 0<=j<S} softmax_j(q_i . k_j / sqrt(D)) v_j - lam[h] * (same with q_diff, k_diff)
+ * with DyT as sa3jax/same_l.py:58-69 and RoPE as sa3jax/same_l.py:92-100; `window` is the reference's band
+ * half-width (`|k - q| <= window`, sa3jax/band_attention.py:110).
+ *   q_dyt, k_dyt : 1 + 2*D floats each: [alpha, gamma[0..D), beta[0..D)]
+ *   cos, sin     : (S, half) floats from hb_rope_tables (ignored when half == 0)
+ *   dtype        : HB_BF16 or HB_F32;  D: 64 or 128;  0 <= half <= D/2;  window >= 0 */
+int hb_band_validate(int dtype, int64_t row_stride, int B, int S, int H, int D, int half, int window);
+int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
+                     const float* q_dyt, const float* k_dyt, const float* cos, const float* sin, int half,
+                     int window, const float* lam, void* out, int B, int S, int H, int D);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HUMMINGBIRD_AMD_H */

@@ -1,0 +1,37 @@
+"""CPU oracle for the two differential-attention kernels. TEST INFRASTRUCTURE ONLY.
+
+This package restates, in NumPy, the arithmetic of the reference's XLA attention paths
+(kelechi-c/hummingbird `sa3jax`), with each function citing the reference file:line it follows:
+
+* `oracle.dense` -- DiT self-attention: RMSNorm -> RoPE -> V-mask -> two softmax attentions -> subtract
+  (sa3jax/dit.py:45-57, 82-119, 122-176, 185-200), plus the fused-kernel cast profile
+  (sa3jax/dense_attention.py:43-101).
+* `oracle.band` -- SAME-L sliding-window attention: DyT -> RoPE -> two band attentions -> subtract
+  (sa3jax/same_l.py:58-69, 84-169), plus the fused-kernel cast profile (sa3jax/band_attention.py:43-120).
+* `oracle.bf16` -- round-to-nearest-even bfloat16 emulation for the cast points.
+
+Only `tests/`, `__graft_entry__.smoke()` and `bench.py`'s CPU-baseline leg may import this package,
+and only as the checker or the timed CPU baseline. The product (`hummingbird_amd`) never imports it.
+
+How each function is pinned (the checks live in tests/test_oracle.py):
+
+* bf16 rounding: against torch's `.to(torch.bfloat16)` (a library routine) on random values, ties and
+  extremes.
+* RMSNorm: unit RMS of the output at w=1, eps=0; scale invariance; eps limit.
+* RoPE tables / rotate-half: against an independent complex-number rotation of the pairs
+  (x[d] + i x[d+half]) * exp(i * theta); norm preservation; inv_freq=0 is the identity; the relative-position
+  property of the rotated dot product.
+* SDPA and the whole dense chain (fp32 profile): against torch.nn.functional.scaled_dot_product_attention in
+  float64 on the CPU (a library routine), plus q=0 -> mean of V, L=1 -> V, key permutation invariance.
+* Differential subtraction: q_d=q, k_d=k gives exactly 0 at lambda=1; linearity in lambda.
+* Band: the grouped three-window restatement (same_l.py:103-148) against brute-force masked attention on the
+  CPU via torch SDPA with an explicit boolean mask; w >= S-1 equals dense unmasked attention; translation
+  equivariance away from the edges.
+* DyT: against torch.tanh; alpha=0 and gamma=0 special cases.
+
+Parity unpinned: the bit-level behaviour of XLA itself (where it rounds einsum outputs, its exp/cos/sin/tanh
+ulps and reduction order) cannot be pinned here because jax is not installed; the oracle fixes the cast
+points the reference's source states, and the tolerance contract (bf16: max-abs <= 2e-2 and cosine >=
+0.9999; fp32: <= 1e-5 relative) absorbs the remaining ulp-level differences.
+"""
+from oracle import band, bf16, dense  # noqa: F401
