@@ -21,8 +21,10 @@ ARCH = "gfx950"
 SOURCES = ("api.cpp", "dense.hip", "band.hip")
 
 # Device flags. Packed fp32 instructions are disabled for every HIP source: hipcc -O3 would otherwise form
-# v_pk_{add,mul,fma}_f32 from ordinary float code.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# v_pk_{add,mul,fma}_f32 from ordinary float code. Floating-point contraction is off so that separately
+# written products and sums keep their own roundings (the reference's cast points, and exact cancellation of
+# identical differential branches); every fused multiply-add in the kernels is an explicit __fmaf_rn.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-ffp-contract=off"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", f"--offload-arch={ARCH}", f"-I{ROOT / 'include'}"]
 
 

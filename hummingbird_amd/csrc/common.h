@@ -69,6 +69,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// The two 8-dim groups of RoPE pair p of a head (rotate_half over the first 2*half dims, half % 8 == 0).
+// With h8 = half / 8 rotary pairs, pair p < h8 couples groups p and p + h8 (dims d and d + half, which
+// rotate_half mixes); the remaining groups are not rotated and are paired in order. A thread that owns one pair
+// therefore has each rotation partner in its own registers.
+__device__ __forceinline__ void pair_groups(int p, int h8, int& m1, int& m2) {
+  if (p < h8) {
+    m1 = p;
+    m2 = p + h8;
+  } else {
+    m1 = 2 * h8 + 2 * (p - h8);
+    m2 = m1 + 1;
+  }
+}
+
 // Workgroup index remap that keeps consecutive logical tiles on one XCD (its own L2). Hardware dispatches
 // workgroup p to XCD p % 8; logical tile `start(x) + p / 8` is given to it, so each XCD walks a contiguous
 // range of the logical order.

@@ -38,6 +38,10 @@ __device__ __forceinline__ SoftmaxPlan dense_plan(const float* __restrict__ qw, 
   return softmax_plan(rd * wave_max(mq), rd * wave_max(mk), D);
 }
 
+// RMSNorm + RoPE of q, k, q_diff, k_diff and V * mask for 64 tokens of one head. Thread task = (token, RoPE
+// group pair): the thread loads the pair's 16 dims of all four q/k sections and the pair's cos/sin slice once,
+// so every load is issued before any arithmetic; the RMS statistic is reduced over the D/16 lanes of a token.
+// RoPE reads the (L, half) fp32 tables; `half` is a multiple of 8 (checked on the host).
 template <int D>
 __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restrict__ qkv, int64_t rs,
                                                        const float* __restrict__ qw, const float* __restrict__ kw,
@@ -45,91 +49,120 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
                                                        const float* __restrict__ sinT, int half,
                                                        const float* __restrict__ vmask, int L, int Lp, int H,
                                                        float eps, int64_t region, uint16_t* __restrict__ ws) {
-  constexpr int CH = D / 8;          // 16-byte chunks per row
-  constexpr int RPP = 256 / CH;      // rows per pass
-  constexpr int PASSES = 64 / RPP;   // passes over the 64-row tile
-  __shared__ float ybuf[64][D + 1];  // RMS-normalised rows (fp32 holding bf16 values) for the rotate-half partner
+  constexpr int PAIRS = D / 16;            // group pairs per row; the lanes of one token are consecutive
+  constexpr int TASKS = 64 * PAIRS / 256;  // (token, pair) tasks per thread
+  constexpr int VCH = 64 * D / 8 / 256;    // 16-byte V chunks per thread
   __shared__ __attribute__((aligned(16))) uint16_t vts[D][64];
 
   const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x;
-  const int ch = t % CH, rsub = t / CH;
   const int l0 = tile * 64;
   const int64_t bh = static_cast<int64_t>(b) * H + h;
   const int64_t HD = static_cast<int64_t>(H) * D;
+  const int h8 = half / 8;
   const float qscale = dense_plan<D>(qw, kw).qscale;
 
-  // q, k, q_diff, k_diff: sections 0, 1, 3, 4 of qkv; workspace regions 0..3.
-  for (int si = 0; si < 4; ++si) {
-    const int sec = si < 2 ? si : si + 1;
-    const bool isq = (si & 1) == 0;
-    const float* w = isq ? qw : kw;
-    float y[PASSES][8];
+  // Issue every global load first: 4 sections x 2 groups of data, the cos/sin slice and the V chunks.
+  u32x4 raw[TASKS][4][2];
+  f32x4 cs[TASKS][4];
+  int tm1[TASKS], tm2[TASKS];
+  bool trot[TASKS];
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int row = p * RPP + rsub, l = l0 + row;
-      float x[8];
-      if (l < L) {
-        unpack8(ld16(qkv + (static_cast<int64_t>(b) * L + l) * rs + sec * HD + h * D + ch * 8), x);
-      } else {
+  for (int i = 0; i < TASKS; ++i) {
+    const int task = t + 256 * i, p = task % PAIRS, l = l0 + task / PAIRS;
+    pair_groups(p, h8, tm1[i], tm2[i]);
+    trot[i] = p < h8;
+    const uint16_t* row = qkv + (static_cast<int64_t>(b) * L + (l < L ? l : 0)) * rs + h * D;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = 0.f;
-      }
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss = __fmaf_rn(x[i], x[i], ss);
-#pragma unroll
-      for (int off = 1; off < CH; off <<= 1) ss += __shfl_xor(ss, off, kWave);
-      const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        y[p][i] = round_bf16(__fmul_rn(__fmul_rn(x[i], inv), w[ch * 8 + i]));
-        ybuf[row][ch * 8 + i] = y[p][i];
-      }
+    for (int si = 0; si < 4; ++si) {
+      const int sec = si < 2 ? si : si + 1;  // q, k, q_diff, k_diff
+      raw[i][si][0] = l < L ? ld16(row + sec * HD + 8 * tm1[i]) : u32x4{0u, 0u, 0u, 0u};
+      raw[i][si][1] = l < L ? ld16(row + sec * HD + 8 * tm2[i]) : u32x4{0u, 0u, 0u, 0u};
     }
-    __syncthreads();
-    uint16_t* dst = ws + si * region + (bh * Lp + l0) * D;
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int row = p * RPP + rsub, l = l0 + row;
-      float o[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int d = ch * 8 + i;
-        float r = y[p][i];
-        if (d < 2 * half && l < L) {
-          const int j = d < half ? d : d - half;
-          const float c = cosT[static_cast<int64_t>(l) * half + j];
-          const float s = sinT[static_cast<int64_t>(l) * half + j];
-          const float partner = d < half ? -ybuf[row][d + half] : ybuf[row][d - half];
-          r = __fadd_rn(__fmul_rn(y[p][i], c), __fmul_rn(partner, s));
-        }
-        r = round_bf16(r);
-        if (isq) r = round_bf16(__fmul_rn(r, qscale));
-        o[i] = l < L ? r : 0.f;
-      }
-      st16(dst + static_cast<int64_t>(row) * D + ch * 8, pack8(o));
+    if (trot[i] && l < L) {
+      const float* c = cosT + static_cast<int64_t>(l) * half + 8 * tm1[i];
+      const float* s = sinT + static_cast<int64_t>(l) * half + 8 * tm1[i];
+      cs[i][0] = *reinterpret_cast<const f32x4*>(c);
+      cs[i][1] = *reinterpret_cast<const f32x4*>(c + 4);
+      cs[i][2] = *reinterpret_cast<const f32x4*>(s);
+      cs[i][3] = *reinterpret_cast<const f32x4*>(s + 4);
     }
-    __syncthreads();
+  }
+  u32x4 vraw[VCH];
+  float vm[VCH];
+#pragma unroll
+  for (int i = 0; i < VCH; ++i) {
+    const int ch = t + 256 * i, l = l0 + ch / (D / 8), col = (ch % (D / 8)) * 8;
+    vraw[i] = l < L ? ld16(qkv + (static_cast<int64_t>(b) * L + l) * rs + 2 * HD + h * D + col)
+                    : u32x4{0u, 0u, 0u, 0u};
+    vm[i] = l < L ? (vmask ? vmask[static_cast<int64_t>(b) * L + l] : 1.f) : 0.f;
   }
 
-  // V * mask, transposed into (D, 64) with the MFMA key permutation.
 #pragma unroll
-  for (int p = 0; p < PASSES; ++p) {
-    const int row = p * RPP + rsub, l = l0 + row;
-    float x[8];
-    if (l < L) {
-      unpack8(ld16(qkv + (static_cast<int64_t>(b) * L + l) * rs + 2 * HD + h * D + ch * 8), x);
-      const float m = vmask ? vmask[static_cast<int64_t>(b) * L + l] : 1.f;
+  for (int i = 0; i < TASKS; ++i) {
+    const int task = t + 256 * i, l = l0 + task / PAIRS;
+    const int m1 = tm1[i], m2 = tm2[i];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = __fmul_rn(x[i], m);
-    } else {
+    for (int si = 0; si < 4; ++si) {
+      const bool isq = (si & 1) == 0;
+      const float* w = isq ? qw : kw;
+      float x1[8], x2[8];
+      unpack8(raw[i][si][0], x1);
+      unpack8(raw[i][si][1], x2);
+      float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = 0.f;
+      for (int j = 0; j < 8; ++j) ss = __fmaf_rn(x2[j], x2[j], __fmaf_rn(x1[j], x1[j], ss));
+#pragma unroll
+      for (int off = 1; off < PAIRS; off <<= 1) ss += __shfl_xor(ss, off, kWave);
+      const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
+      float y1[8], y2[8], o1[8], o2[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {  // RMSNorm (dit.py:56-57): x * rsqrt(mean + eps), * w, cast
+        y1[j] = round_bf16((x1[j] * inv) * w[8 * m1 + j]);
+        y2[j] = round_bf16((x2[j] * inv) * w[8 * m2 + j]);
+      }
+      if (trot[i]) {
+        const float c[8] = {cs[i][0][0], cs[i][0][1], cs[i][0][2], cs[i][0][3],
+                            cs[i][1][0], cs[i][1][1], cs[i][1][2], cs[i][1][3]};
+        const float s[8] = {cs[i][2][0], cs[i][2][1], cs[i][2][2], cs[i][2][3],
+                            cs[i][3][0], cs[i][3][1], cs[i][3][2], cs[i][3][3]};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {  // rotate_half (dit.py:96-98): d < half takes -x[d+half], else x[d-half]
+          o1[j] = round_bf16(y1[j] * c[j] + (-y2[j]) * s[j]);
+          o2[j] = round_bf16(y2[j] * c[j] + y1[j] * s[j]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          o1[j] = y1[j];
+          o2[j] = y2[j];
+        }
+      }
+      if (isq) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          o1[j] = round_bf16(o1[j] * qscale);
+          o2[j] = round_bf16(o2[j] * qscale);
+        }
+      }
+      if (l >= L) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o1[j] = o2[j] = 0.f;
+      }
+      uint16_t* dst = ws + si * region + (bh * Lp + l) * D;
+      st16(dst + 8 * m1, pack8(o1));
+      st16(dst + 8 * m2, pack8(o2));
     }
-    const int slot = vt_slot(row);
+  }
+
+  // V * mask, transposed into (D, 64) with the MFMA key permutation, then written with 16-byte stores.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vts[ch * 8 + i][slot] = f2bf(x[i]);
+  for (int i = 0; i < VCH; ++i) {
+    const int ch = t + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8, slot = vt_slot(key);
+    float x[8];
+    unpack8(vraw[i], x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) vts[col + j][slot] = f2bf(x[j] * vm[i]);
   }
   __syncthreads();
   uint16_t* dstv = ws + 4 * region + (bh * (Lp / 64) + tile) * (static_cast<int64_t>(D) * 64);
@@ -297,6 +330,9 @@ extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int
   const DenseLayout lay = dense_layout(dtype, B, L, H, D);
   st = dense_args(qkv, q_weight, k_weight, cos, sin, half, workspace, workspace_bytes, lay.total_bytes);
   if (st) return st;
+  if (half % 8 != 0) return fail(HB_ERR_HALF, "dense kernel needs half %% 8 == 0 (half=%d)", half);
+  if (half > 0 && (reinterpret_cast<uintptr_t>(cos) % 16 || reinterpret_cast<uintptr_t>(sin) % 16))
+    return fail(HB_ERR_STRIDE, "cos and sin must be 16-byte aligned");
   if (dtype != HB_BF16) return fail(HB_ERR_DTYPE, "dense fp32 path not built yet");
   const dim3 grid(static_cast<unsigned>(lay.Lp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
   const uint16_t* x = static_cast<const uint16_t*>(qkv);

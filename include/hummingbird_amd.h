@@ -41,7 +41,7 @@ enum hb_status {
   HB_ERR_SHAPE = 2,     /* B, N or H out of range */
   HB_ERR_DTYPE = 3,     /* dtype is not HB_BF16 or HB_F32 */
   HB_ERR_HEAD_DIM = 4,  /* D is not 64 or 128 */
-  HB_ERR_HALF = 5,      /* rotary half-width outside [0, D/2] */
+  HB_ERR_HALF = 5,      /* rotary half-width outside [0, D/2] or not a multiple of 8 */
   HB_ERR_WINDOW = 6,    /* band half-width < 0 */
   HB_ERR_STRIDE = 7,    /* row_stride < 5*H*D, not a multiple of 8, or qkv misaligned */
   HB_ERR_WORKSPACE = 8, /* workspace missing, too small or misaligned */
@@ -77,7 +77,7 @@ int hb_rope_tables(hipStream_t stream, const float* inv_freq, int half, int leng
  *   cos, sin           : (L, half) floats from hb_rope_tables (ignored when half == 0)
  *   vmask              : (B, L) floats, or NULL for all ones
  *   dtype              : HB_BF16 or HB_F32 (of qkv and out)
- *   D                  : 64 or 128;  0 <= half <= D/2;  eps >= 0
+ *   D                  : 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  eps >= 0
  *   workspace          : >= hb_dense_workspace_size(dtype, B, L, H, D) bytes, 256-byte aligned; holds the
  *                        prepared q/k/v for the duration of the call (stream-ordered).
  * Internally two kernels run on `stream`: hb_dense_prep then hb_dense_attend (exported separately below). */
@@ -106,7 +106,7 @@ int hb_dense_attend(hipStream_t stream, const void* workspace, size_t workspace_
  * half-width (`|k - q| <= window`, sa3jax/band_attention.py:110).
  *   q_dyt, k_dyt : 1 + 2*D floats each: [alpha, gamma[0..D), beta[0..D)]
  *   cos, sin     : (S, half) floats from hb_rope_tables (ignored when half == 0)
- *   dtype        : HB_BF16 or HB_F32;  D: 64 or 128;  0 <= half <= D/2;  window >= 0 */
+ *   dtype        : HB_BF16 or HB_F32;  D: 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  window >= 0 */
 int hb_band_validate(int dtype, int64_t row_stride, int B, int S, int H, int D, int half, int window);
 int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
                      const float* q_dyt, const float* k_dyt, const float* cos, const float* sin, int half,

@@ -1,0 +1,109 @@
+"""The C ABI on the CPU: the shared library loads, exports every entry point include/hummingbird_amd.h
+declares, and its host-side validators reject what the reference rejects at trace time. No kernel is
+launched here (no GPU in this environment)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from hummingbird_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "hummingbird_amd.h"
+
+
+def declared_functions() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(hb_[a-z0-9_]+)\s*\(", text))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libhummingbird_amd.so is not built: run `python -m hummingbird_amd._build`")
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for required in ("hb_dense_diffattn", "hb_band_diffattn", "hb_rope_tables", "hb_dense_prep", "hb_dense_attend",
+                     "hb_dense_workspace_size", "hb_dense_validate", "hb_band_validate", "hb_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in declared_functions() if not hasattr(raw, n)]
+    assert not missing, f"declared in the header but not exported: {missing}"
+
+
+def test_python_prototypes_cover_the_header(lib):
+    assert declared_functions() == set(_lib.SIGNATURES)
+
+
+def test_version_and_status_names(lib):
+    assert b"gfx950" in lib.hb_version()
+    assert lib.hb_status_name(0) == b"HB_OK"
+    assert lib.hb_status_name(2) == b"HB_ERR_SHAPE"
+    assert lib.hb_status_name(999) == b"HB_ERR_UNKNOWN"
+
+
+DENSE_OK = dict(dtype=0, row_stride=5 * 24 * 64, B=2, L=2584, H=24, D=64, half=32, eps=1e-6)
+
+
+def dense_validate(lib, **kw):
+    a = dict(DENSE_OK, **kw)
+    return lib.hb_dense_validate(a["dtype"], a["row_stride"], a["B"], a["L"], a["H"], a["D"], a["half"], a["eps"])
+
+
+@pytest.mark.parametrize("kw,status", [
+    ({}, 0),
+    ({"D": 128, "H": 12, "row_stride": 5 * 12 * 128, "half": 64}, 0),
+    ({"D": 96}, 4),                       # head_dim (reference: dense_attention.py:119-120)
+    ({"half": 33}, 5), ({"half": -1}, 5),
+    ({"dtype": 7}, 3),
+    ({"row_stride": 100}, 7), ({"row_stride": 5 * 24 * 64 + 4}, 7),
+    ({"L": 0}, 2), ({"B": 0}, 2), ({"H": 0}, 2),
+    ({"eps": -1.0}, 10), ({"eps": float("nan")}, 10),
+])
+def test_dense_validate(lib, kw, status):
+    assert dense_validate(lib, **kw) == status
+    if status:
+        assert lib.hb_last_error()  # a message is recorded
+
+
+@pytest.mark.parametrize("kw,status", [
+    ({}, 0), ({"window": 0}, 0), ({"window": -1}, 6), ({"D": 32}, 4), ({"half": 40}, 5),
+])
+def test_band_validate(lib, kw, status):
+    a = {**dict(dtype=0, row_stride=5 * 8 * 64, B=1, S=82688, H=8, D=64, half=32, window=128), **kw}
+    assert lib.hb_band_validate(a["dtype"], a["row_stride"], a["B"], a["S"], a["H"], a["D"], a["half"],
+                                a["window"]) == status
+
+
+def test_workspace_size(lib):
+    # five (B, H, Lp, D) bf16 regions with L padded to the 128-query block
+    assert lib.hb_dense_workspace_size(0, 2, 2584, 24, 64) == 5 * 2 * 24 * 2688 * 64 * 2
+    assert lib.hb_dense_workspace_size(1, 1, 1, 1, 64) == 5 * 128 * 64 * 4
+    assert lib.hb_dense_workspace_size(0, 1, 1, 1, 96) == 0
+
+
+def test_null_pointers_are_rejected_before_any_launch(lib):
+    # every pointer NULL: the launcher must return HB_ERR_NULL without touching the GPU
+    st = lib.hb_dense_diffattn(None, None, 0, 5 * 64, None, None, None, None, 0, None, None, None, 1, 8, 1, 64,
+                               1e-6, None, 0)
+    assert st == 1
+    st = lib.hb_band_diffattn(None, None, 0, 5 * 64, None, None, None, None, 0, 4, None, None, 1, 8, 1, 64)
+    assert st == 1
+    assert lib.hb_rope_tables(None, None, 4, 10, None, None) == 1
+    assert lib.hb_rope_tables(None, None, 0, 10, None, None) == 0  # nothing to build
+
+
+def test_errors_map_to_python_exceptions(lib):
+    with pytest.raises(ValueError, match="HB_ERR_HEAD_DIM"):
+        _lib.check(dense_validate(lib, D=96), "dense")
+    with pytest.raises(TypeError):
+        _lib.check(dense_validate(lib, dtype=7), "dense")
