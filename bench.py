@@ -39,6 +39,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-iters", type=int, default=50, help="launches per live kernel timing")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the per-kernel timing loops plus one 256 MiB device copy (the traffic-counter "
+                         "calibration kernel); for profiling under rocprofv3")
     return ap.parse_args()
 
 
@@ -154,20 +157,28 @@ def main() -> int:
         for _ in range(wl.BAND_CALLS_PER_CLIP):
             band_call()
 
-    print(f"[bench] warmup {args.warmup} clip(s)", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    print(f"[bench] timing {args.steps} clip(s)", file=sys.stderr, flush=True)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_host = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        step()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    host_s = time.perf_counter() - t_host
-    ms_clip = start.elapsed_time(stop) / args.steps
+    if args.kernels_only:
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # 256 MiB read + 256 MiB written: calibrates FETCH_SIZE / WRITE_SIZE
+        torch.cuda.synchronize()
+        del src, dst
+        ms_clip, host_s = float("nan"), 0.0
+    else:
+        print(f"[bench] warmup {args.warmup} clip(s)", file=sys.stderr, flush=True)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        print(f"[bench] timing {args.steps} clip(s)", file=sys.stderr, flush=True)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_host = time.perf_counter()
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        host_s = time.perf_counter() - t_host
+        ms_clip = start.elapsed_time(stop) / args.steps
 
     # ---- live per-kernel timing (HIP events on the launch stream) ----
     def timed(fn, n: int) -> float:
@@ -224,7 +235,7 @@ def main() -> int:
         # prep reads the 5 qkv sections and writes them back prepared: 2 x 5 H D bf16 per token
         "dense_prep": {"avg_us": round(prep_s * 1e6, 2), "gbs": round(2 * B * L * 5 * H * D * 2 / prep_s / 1e9, 1)},
     }
-    if not args.no_cpu:
+    if not args.no_cpu and not args.kernels_only:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result), flush=True)

@@ -19,9 +19,9 @@ constexpr int kDenseKeyTile = 64;
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-// The dense workspace holds five equally sized regions: q', k', q_diff', k_diff' as (B, H, Lp, D) and V as
-// (B, H, Lp/64, D, 64) (transposed 64-key tiles, keys permuted inside each 16-key group to match the MFMA
-// operand order), Lp = L rounded up to kDenseQueryBlock. Elements are bf16 for HB_BF16 and fp32 for HB_F32.
+// The dense workspace holds five equally sized (B, H, Lp, D) regions of prepared (normalised, rotated or
+// masked) rows, Lp = L rounded up to kDenseQueryBlock and zero-filled past L. Elements are bf16
+// for HB_BF16 and fp32 for HB_F32. Region order: q', k', q_diff', k_diff', v'.
 struct DenseLayout {
   int64_t Lp;
   int64_t region_elems;  // B * H * Lp * D

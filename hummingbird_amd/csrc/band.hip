@@ -4,15 +4,18 @@
 // sa3jax/same_l.py:151-169, in one pass over qkv.
 //
 // Work split. One workgroup (8 waves, 512 threads) owns 256 consecutive queries of one (batch, head); each
-// wave holds 32 of them in registers as MFMA B operands. The keys that can reach the block,
+// wave attends 32 of them. The keys that can reach the block,
 // [q0 - w, q0 + 256 + w) clipped to [0, S), stream through LDS in 64-key tiles, double-buffered with one
 // barrier per tile:
 //   - waves 0-3 prepare K and K_diff of the tile: DyT (same_l.py:58-69, fp32) and rotate-half RoPE
 //     (same_l.py:92-100, fp32), one bf16 rounding; each thread owns a pair of 8-dim groups that RoPE couples
 //     (d and d + half), so the rotation partner is in the thread's own registers and the cos/sin row is
 //     loaded once for k and k_diff;
-//   - waves 4-7 transpose the tile's V rows into the MFMA A-operand order;
-//   - the raw rows of the next tile are loaded into registers while the current tile is attended;
+//   - waves 4-7 copy the tile's V rows (row-major; the MFMA operand is read with transposing LDS loads);
+//   - the raw rows of the next tile are loaded into registers while the current tile is attended (the cos/sin
+//     slices, shared by all heads and L2-resident, are read at prep time);
+//   - q and q_diff of the block stay in LDS (prepared once) and are re-read as MFMA B operands each tile, which
+//     keeps the register budget within two waves per SIMD;
 //   - every wave then attends the tile if it intersects its band: unmasked when the tile lies inside
 //     `|k - q| <= w` for all its 32 queries, masked per score on the band edges (band_attention.py:108-110).
 // Scores, softmax and both branches follow attn_tile.h; the subtraction is fp32 with one cast
@@ -34,15 +37,18 @@ struct BandCfg {
   static constexpr int NT = 64 * NW;        // threads
   static constexpr int QB = 32 * NW;        // queries per workgroup
   static constexpr int KT = 64;             // keys per tile
-  static constexpr int KP = D + 8;          // K / Q row pitch (elements)
-  static constexpr int VP = KT + 8;         // V^T row pitch
+  static constexpr int KP = D + 8;          // K / K_diff / V / Q row pitch (elements)
   static constexpr int K_ELEMS = KT * KP;
-  static constexpr int STAGE = 2 * K_ELEMS + D * VP;  // K, K_diff, V^T of one tile
-  static constexpr int QSTAGE = 2 * QB * KP;          // q, q_diff of the block (start only)
-  static constexpr int LDS_ELEMS = 2 * STAGE > QSTAGE ? 2 * STAGE : QSTAGE;
+  static constexpr int STAGE = 3 * K_ELEMS;           // K, K_diff, V of one tile, all row-major
+  static constexpr int QSTAGE = 2 * QB * KP;          // q, q_diff of the block
+  // D = 64: q stays in LDS and is re-read every tile (keeps two waves per SIMD without spills).
+  // D = 128: q does not fit beside the tiles; it is staged through the tile buffers into registers.
+  static constexpr bool Q_IN_LDS = D == 64;
+  static constexpr int TILE_BASE = Q_IN_LDS ? QSTAGE : 0;
+  static constexpr int LDS_ELEMS = Q_IN_LDS ? QSTAGE + 2 * STAGE : (QSTAGE > 2 * STAGE ? QSTAGE : 2 * STAGE);
   static constexpr int PAIRS = D / 16;                // 16-dim group pairs per row
   static constexpr int KTASK = KT * PAIRS / 256;      // (key, pair) tasks per prep thread (waves 0-3)
-  static constexpr int VTASK = KT * D / 8 / 256;      // 16-byte V chunks per transpose thread (waves 4-7)
+  static constexpr int VTASK = KT * D / 8 / 256;      // 16-byte V chunks per copy thread (waves 4-7)
   static constexpr int QTASK = QB * PAIRS / NT;       // (query, pair) tasks per thread at the start
 };
 
@@ -53,25 +59,28 @@ struct PairRaw {
   f32x4 c0, c1, s0, s1;  // cos / sin of the 8 rotary frequencies 8*m1 .. 8*m1+7
 };
 
-__device__ __forceinline__ void load_pair(PairRaw& r, const uint16_t* __restrict__ rowA,
-                                          const uint16_t* __restrict__ rowB, const float* __restrict__ cosT,
-                                          const float* __restrict__ sinT, int pos, int S, int half, int m1, int m2,
-                                          bool rot) {
+__device__ __forceinline__ void load_rows(PairRaw& r, const uint16_t* __restrict__ rowA,
+                                          const uint16_t* __restrict__ rowB, int pos, int S, int m1, int m2) {
   if (pos >= 0 && pos < S) {
     r.a1 = ld16(rowA + 8 * m1);
     r.a2 = ld16(rowA + 8 * m2);
     r.b1 = ld16(rowB + 8 * m1);
     r.b2 = ld16(rowB + 8 * m2);
-    if (rot) {
-      const float* c = cosT + static_cast<int64_t>(pos) * half + 8 * m1;
-      const float* s = sinT + static_cast<int64_t>(pos) * half + 8 * m1;
-      r.c0 = *reinterpret_cast<const f32x4*>(c);
-      r.c1 = *reinterpret_cast<const f32x4*>(c + 4);
-      r.s0 = *reinterpret_cast<const f32x4*>(s);
-      r.s1 = *reinterpret_cast<const f32x4*>(s + 4);
-    }
   } else {
     r.a1 = r.a2 = r.b1 = r.b2 = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+__device__ __forceinline__ void load_table(PairRaw& r, const float* __restrict__ cosT,
+                                           const float* __restrict__ sinT, int pos, int S, int half, int m1,
+                                           bool rot) {
+  if (rot && pos >= 0 && pos < S) {
+    const float* c = cosT + static_cast<int64_t>(pos) * half + 8 * m1;
+    const float* s = sinT + static_cast<int64_t>(pos) * half + 8 * m1;
+    r.c0 = *reinterpret_cast<const f32x4*>(c);
+    r.c1 = *reinterpret_cast<const f32x4*>(c + 4);
+    r.s0 = *reinterpret_cast<const f32x4*>(s);
+    r.s1 = *reinterpret_cast<const f32x4*>(s + 4);
   }
 }
 
@@ -133,21 +142,22 @@ __device__ __forceinline__ float dyt_norm_bound(const float* __restrict__ dyt) {
   return sqrtf(acc);
 }
 
-template <int D, bool FAST>
+template <int D, bool FAST, class QFrag>
 __device__ __forceinline__ void band_loop(const uint16_t* __restrict__ xb, int64_t rs, int64_t HD, int h, int S,
                                           int window, int half, int q0, const float* __restrict__ cosT,
                                           const float* __restrict__ sinT, float ka2, const float* sdyt_kg,
-                                          const float* sdyt_kb, uint16_t* smem, const u32x4 (&qf)[2][D / 16],
-                                          f32x16 (&o)[2][D / 32], float (&lsum)[2], float c) {
+                                          const float* sdyt_kb, uint16_t* smem, QFrag qf,
+                                          f32x16 (&o)[2][1][D / 32], float (&lsum)[2][1], float c) {
   using C = BandCfg<D>;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, lr = lane & 31;
+  const int t = threadIdx.x, lane = t & 63, wave = wave_id(), lr = lane & 31;
   const int h8 = half / 8;
-  float m[2] = {-INFINITY, -INFINITY};
+  float m[2][1] = {{-INFINITY}, {-INFINITY}};
+  uint16_t* tiles = smem + C::TILE_BASE;
   const int qa = q0 + 32 * wave;  // this wave's first query
   const int q = qa + lr;           // this lane's query
   const int kbeg = q0 - window > 0 ? q0 - window : 0;
   const int kend = q0 + C::QB + window < S ? q0 + C::QB + window : S;
-  const bool producer = wave < 4;  // waves 0-3 prepare K / K_diff, waves 4-7 transpose V
+  const bool producer = wave < 4;  // waves 0-3 prepare K / K_diff, waves 4-7 copy V
   const int pt = t & 255;          // thread index inside its half of the workgroup
 
   // Per-thread task geometry (fixed for every tile).
@@ -169,7 +179,7 @@ __device__ __forceinline__ void band_loop(const uint16_t* __restrict__ xb, int64
       for (int i = 0; i < C::KTASK; ++i) {
         const int pos = kt0 + tk_key[i];
         const uint16_t* row = xb + static_cast<int64_t>(pos) * rs + h * D;
-        load_pair(kraw[i], row + 1 * HD, row + 4 * HD, cosT, sinT, pos, S, half, tk_m1[i], tk_m2[i], tk_rot[i]);
+        load_rows(kraw[i], row + 1 * HD, row + 4 * HD, pos, S, tk_m1[i], tk_m2[i]);
       }
     } else {
 #pragma unroll
@@ -181,26 +191,24 @@ __device__ __forceinline__ void band_loop(const uint16_t* __restrict__ xb, int64
   };
   auto prep = [&](int kt0, uint16_t* s) {
     if (producer) {
+      const int z = opaque_zero();  // re-read gamma/beta every tile rather than pin 32 registers for them
 #pragma unroll
       for (int i = 0; i < C::KTASK; ++i) {
         const int pos = kt0 + tk_key[i];
         const bool in = pos < S;
+        load_table(kraw[i], cosT, sinT, pos, S, half, tk_m1[i], tk_rot[i]);  // L2-resident, read at prep time
         uint16_t* rowK = s + tk_key[i] * C::KP;
-        prep_pair(kraw[i].a1, kraw[i].a2, kraw[i], tk_rot[i], in, ka2, sdyt_kg, sdyt_kb, tk_m1[i], tk_m2[i], 1.f,
-                  rowK);
-        prep_pair(kraw[i].b1, kraw[i].b2, kraw[i], tk_rot[i], in, ka2, sdyt_kg, sdyt_kb, tk_m1[i], tk_m2[i], 1.f,
-                  rowK + C::K_ELEMS);
+        prep_pair(kraw[i].a1, kraw[i].a2, kraw[i], tk_rot[i], in, ka2, sdyt_kg + z, sdyt_kb + z, tk_m1[i],
+                  tk_m2[i], 1.f, rowK);
+        prep_pair(kraw[i].b1, kraw[i].b2, kraw[i], tk_rot[i], in, ka2, sdyt_kg + z, sdyt_kb + z, tk_m1[i],
+                  tk_m2[i], 1.f, rowK + C::K_ELEMS);
       }
     } else {
-      uint16_t* vt = s + 2 * C::K_ELEMS;
+      uint16_t* sv = s + 2 * C::K_ELEMS;
 #pragma unroll
       for (int i = 0; i < C::VTASK; ++i) {
-        const int ch = pt + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8, slot = vt_slot(key);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          vt[(col + 2 * j) * C::VP + slot] = static_cast<uint16_t>(vraw[i][j] & 0xffffu);
-          vt[(col + 2 * j + 1) * C::VP + slot] = static_cast<uint16_t>(vraw[i][j] >> 16);
-        }
+        const int ch = pt + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8;
+        *reinterpret_cast<u32x4*>(sv + key * C::KP + col) = vraw[i];
       }
     }
   };
@@ -208,24 +216,21 @@ __device__ __forceinline__ void band_loop(const uint16_t* __restrict__ xb, int64
   if (kbeg < kend) gload(kbeg);
   int stage = 0;
   for (int kt0 = kbeg; kt0 < kend; kt0 += C::KT, stage ^= 1) {
-    uint16_t* s = smem + stage * C::STAGE;
+    uint16_t* s = tiles + stage * C::STAGE;
     prep(kt0, s);
     if (kt0 + C::KT < kend) gload(kt0 + C::KT);
     __syncthreads();
 
-    // Wave-uniform band classification of this tile against the wave's 32 queries.
+    // Wave-uniform band classification of this tile against the wave's 32 queries: skipped when it lies
+    // outside the band, unmasked when `|k - q| <= w` holds for every pair, masked per score otherwise.
     const int klast = kt0 + C::KT - 1;
     if (kt0 <= qa + 31 + window && klast >= qa - window) {
-      if (kt0 >= qa + 31 - window && klast <= qa + window && klast < S) {
-        attend_tile<D, FAST, false>(s, s + C::K_ELEMS, s + 2 * C::K_ELEMS, C::KP, C::VP, qf, o, lsum, m, c,
-                                    [](int) { return true; });
-      } else {
-        attend_tile<D, FAST, true>(s, s + C::K_ELEMS, s + 2 * C::K_ELEMS, C::KP, C::VP, qf, o, lsum, m, c,
-                                   [&](int k) {
-                                     const int key = kt0 + k, dist = key - q;
-                                     return key < S && dist <= window && dist >= -window;
-                                   });
-      }
+      const bool inside = kt0 >= qa + 31 - window && klast <= qa + window && klast < S;
+      attend_tile<D, 2, 1, FAST>([&](int br) { return s + br * C::K_ELEMS; }, s + 2 * C::K_ELEMS, C::KP, C::KP,
+                                 qf, o, lsum, m, c, !inside, [&](int k, int) {
+                             const int key = kt0 + k, dist = key - q;
+                             return (key < S) & (dist <= window) & (dist >= -window);
+                           });
     }
   }
 }
@@ -242,9 +247,12 @@ __global__ __launch_bounds__(512) void band_attend_bf16(const uint16_t* __restri
   __shared__ __attribute__((aligned(16))) uint16_t smem[C::LDS_ELEMS];
   __shared__ float sdyt[4 * D];  // q gamma, q beta, k gamma, k beta
   const int nqb = (S + C::QB - 1) / C::QB;
+  // Logical order: query block major, (batch, head) minor. Each XCD walks a contiguous range, so the heads of a
+  // query block (which read the same RoPE table rows) and its neighbours (which share the key halo) run
+  // together on one XCD and meet in its L2.
   const int tile = xcd_remap(blockIdx.x, B * H * nqb);
-  const int qb = tile % nqb, bh = tile / nqb, h = bh % H, b = bh / H;
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, lr = lane & 31, lh = lane >> 5;
+  const int qb = tile / (B * H), bh = tile % (B * H), h = bh % H, b = bh / H;
+  const int t = threadIdx.x, lane = t & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
   const int q0 = qb * C::QB;
   const int64_t HD = static_cast<int64_t>(H) * D;
   const uint16_t* xb = qkv + static_cast<int64_t>(b) * S * rs;
@@ -269,36 +277,50 @@ __global__ __launch_bounds__(512) void band_attend_bf16(const uint16_t* __restri
     const bool rot = p < h8;
     PairRaw r;
     const uint16_t* src = xb + static_cast<int64_t>(pos) * rs + h * D;
-    load_pair(r, src, src + 3 * HD, cosT, sinT, pos, S, half, m1, m2, rot);
+    load_rows(r, src, src + 3 * HD, pos, S, m1, m2);
+    load_table(r, cosT, sinT, pos, S, half, m1, rot);
     const bool in = pos < S;
     prep_pair(r.a1, r.a2, r, rot, in, qa2, sdyt, sdyt + D, m1, m2, plan.qscale, smem + row * C::KP);
     prep_pair(r.b1, r.b2, r, rot, in, qa2, sdyt, sdyt + D, m1, m2, plan.qscale, smem + (C::QB + row) * C::KP);
   }
-  __syncthreads();
-  u32x4 qf[2][D / 16];
+  f32x16 o[2][1][D / 32];
 #pragma unroll
   for (int br = 0; br < 2; ++br)
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-      qf[br][kk] = lds16(smem + (br * C::QB + 32 * wave + lr) * C::KP + 16 * kk + 8 * lh);
-  __syncthreads();
-
-  f32x16 o[2][D / 32];
+    for (int dt = 0; dt < D / 32; ++dt) o[br][0][dt] = f32x16{};
+  float lsum[2][1] = {{0.f}, {0.f}};
+  if constexpr (C::Q_IN_LDS) {
+    // the first barrier inside band_loop publishes the staged q rows
+    const uint16_t* sq = smem + (32 * wave + lr) * C::KP + 8 * lh;  // this lane's query row (branch 0)
+    // the opaque zero keeps these loop-invariant reads inside the tile loop instead of pinning 32 registers
+    auto qf = [=](int br, int, int kk) { return lds16(sq + opaque_zero() + br * C::QB * C::KP + 16 * kk); };
+    if (plan.fast)
+      band_loop<D, true>(xb, rs, HD, h, S, window, half, q0, cosT, sinT, ka2, sdyt + 2 * D, sdyt + 3 * D, smem, qf,
+                         o, lsum, plan.c);
+    else
+      band_loop<D, false>(xb, rs, HD, h, S, window, half, q0, cosT, sinT, ka2, sdyt + 2 * D, sdyt + 3 * D, smem, qf,
+                          o, lsum, plan.c);
+  } else {
+    __syncthreads();
+    u32x4 qr[2][D / 16];
 #pragma unroll
-  for (int br = 0; br < 2; ++br)
+    for (int br = 0; br < 2; ++br)
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) o[br][dt] = f32x16{};
-  float lsum[2] = {0.f, 0.f};
-  if (plan.fast)
-    band_loop<D, true>(xb, rs, HD, h, S, window, half, q0, cosT, sinT, ka2, sdyt + 2 * D, sdyt + 3 * D, smem, qf, o,
-                       lsum, plan.c);
-  else
-    band_loop<D, false>(xb, rs, HD, h, S, window, half, q0, cosT, sinT, ka2, sdyt + 2 * D, sdyt + 3 * D, smem, qf, o,
-                        lsum, plan.c);
+      for (int kk = 0; kk < D / 16; ++kk)
+        qr[br][kk] = lds16(smem + (br * C::QB + 32 * wave + lr) * C::KP + 16 * kk + 8 * lh);
+    __syncthreads();  // the tile buffers alias the staging area
+    auto qf = [&](int br, int, int kk) { return qr[br][kk]; };
+    if (plan.fast)
+      band_loop<D, true>(xb, rs, HD, h, S, window, half, q0, cosT, sinT, ka2, sdyt + 2 * D, sdyt + 3 * D, smem, qf,
+                         o, lsum, plan.c);
+    else
+      band_loop<D, false>(xb, rs, HD, h, S, window, half, q0, cosT, sinT, ka2, sdyt + 2 * D, sdyt + 3 * D, smem, qf,
+                          o, lsum, plan.c);
+  }
 
   const int q = q0 + 32 * wave + lr;
   uint16_t* orow = q < S ? out + (static_cast<int64_t>(b) * S + q) * HD + h * D : nullptr;
-  store_diff_bf16<D>(orow, o, lsum, lam ? lam[h] : 1.f);
+  store_diff_bf16<D, 1>(orow, o, lsum, 0, lam ? lam[h] : 1.f);
 }
 
 }  // namespace hb

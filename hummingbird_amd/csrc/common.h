@@ -63,6 +63,18 @@ __device__ __forceinline__ float add_bf16_pair(uint32_t p, float acc) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A zero the compiler cannot see through. Adding it to an address inside a loop keeps loop-invariant loads
+// in the loop (where their registers are short-lived) instead of hoisted and held across the whole loop.
+__device__ __forceinline__ int opaque_zero() {
+  int z;
+  asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+  return z;
+}
+
+// Index of this wave inside the workgroup as a scalar: branches on it become scalar branches instead of
+// exec-masked diamonds (the compiler cannot prove threadIdx.x / 64 uniform on its own).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));

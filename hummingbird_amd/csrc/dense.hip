@@ -5,8 +5,8 @@
 //
 //   dense_prep    one pass over qkv: per-head RMSNorm (dit.py:45-57) and rotate-half RoPE (dit.py:90-98) of
 //                 q, k, q_diff, k_diff, V * mask (dit.py:174-175), written in bf16 to a workspace. q and
-//                 q_diff also carry log2(e)/sqrt(D) so the attention kernel can use exp2 directly. V is stored
-//                 as transposed 64-key tiles so it can feed the MFMA A operand with one 16-byte LDS read.
+//                 q_diff also carry the softmax scale (SoftmaxPlan). V stays row-major; the attention kernel
+//                 reads its MFMA operand with gfx950's transposing LDS loads.
 //   dense_attend  flash-style single pass per (batch, head, 128-query block): K, K_diff and V tiles of 64 keys
 //                 are double-buffered through LDS; S^T = K Q^T and O^T += V^T P^T on
 //                 v_mfma_f32_32x32x16_bf16 with fp32 accumulation; both branches share each V tile; scores
@@ -52,8 +52,6 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
   constexpr int PAIRS = D / 16;            // group pairs per row; the lanes of one token are consecutive
   constexpr int TASKS = 64 * PAIRS / 256;  // (token, pair) tasks per thread
   constexpr int VCH = 64 * D / 8 / 256;    // 16-byte V chunks per thread
-  __shared__ __attribute__((aligned(16))) uint16_t vts[D][64];
-
   const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int t = threadIdx.x;
   const int l0 = tile * 64;
@@ -155,129 +153,194 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     }
   }
 
-  // V * mask, transposed into (D, 64) with the MFMA key permutation, then written with 16-byte stores.
+  // V * mask, row-major like k (the attention kernel reads it with transposing LDS loads).
 #pragma unroll
   for (int i = 0; i < VCH; ++i) {
-    const int ch = t + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8, slot = vt_slot(key);
+    const int ch = t + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8;
     float x[8];
     unpack8(vraw[i], x);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) vts[col + j][slot] = f2bf(x[j] * vm[i]);
-  }
-  __syncthreads();
-  uint16_t* dstv = ws + 4 * region + (bh * (Lp / 64) + tile) * (static_cast<int64_t>(D) * 64);
-#pragma unroll
-  for (int j = 0; j < D / 32; ++j) {
-    const int c = t + 256 * j, d = c >> 3, col = (c & 7) * 8;
-    st16(dstv + d * 64 + col, *reinterpret_cast<const u32x4*>(&vts[d][col]));
+    for (int j = 0; j < 8; ++j) x[j] *= vm[i];
+    st16(ws + 4 * region + (bh * Lp + l0 + key) * D + col, pack8(x));
   }
 }
 
+// Attention tiling: a workgroup of 4 waves attends 128 queries. D = 64: each wave owns one differential branch
+// of 64 queries (two MFMA column tiles), so every K fragment read from LDS feeds two MFMAs while a wave's
+// registers still fit two waves per SIMD; waves 0-1 run branch 1 (q, k) and waves 2-3 branch 2 (q_diff,
+// k_diff), and the second pair hands its normalised result to the first through LDS at the end. D = 128: each
+// wave owns both branches of 32 queries.
 template <int D>
 struct DenseTile {
-  static constexpr int KP = D + 8;   // K row pitch in elements (144 B for D = 64)
-  static constexpr int VP = 64 + 8;  // V^T row pitch in elements
+  static constexpr bool SPLIT = D == 64;   // one branch per wave
+  static constexpr int NB = SPLIT ? 1 : 2;  // branches per wave
+  static constexpr int NCT = SPLIT ? 2 : 1; // 32-query column tiles per wave
+  static constexpr int NT = 256;            // threads per workgroup
+  static constexpr int KP = D + 8;          // K, K_diff and V row pitch in elements (144 B for D = 64)
   static constexpr int K_ELEMS = 64 * KP;
-  static constexpr int V_ELEMS = D * VP;
-  static constexpr int STAGE = 2 * K_ELEMS + V_ELEMS;
-  static constexpr int NCH = D / 32;  // 16-byte chunks per thread per 64-key tile of one tensor
+  static constexpr int STAGE = 3 * K_ELEMS; // K, K_diff, V of one 64-key tile, all row-major
+  static constexpr int NCH = 64 * D / 8 / NT;  // 16-byte chunks per thread per 64-key tile of one tensor
 };
 
 template <int D, bool FAST>
 __device__ __forceinline__ void dense_attend_loop(const uint16_t* __restrict__ Kb, const uint16_t* __restrict__ Kdb,
-                                                  const uint16_t* __restrict__ Vb, int L, uint16_t* smem,
-                                                  const u32x4 (&qf)[2][D / 16], f32x16 (&o)[2][D / 32],
-                                                  float (&lsum)[2], float c) {
+                                                  const uint16_t* __restrict__ Vb, int L, int br0, uint16_t* smem,
+                                                  const u32x4 (&qf)[DenseTile<D>::NB][DenseTile<D>::NCT][D / 16],
+                                                  f32x16 (&o)[DenseTile<D>::NB][DenseTile<D>::NCT][D / 32],
+                                                  float (&lsum)[DenseTile<D>::NB][DenseTile<D>::NCT], float c) {
   using T = DenseTile<D>;
+  constexpr int NB = T::NB, NCT = T::NCT;
   const int tid = threadIdx.x;
   const int nkt = (L + 63) / 64;
-  float m[2] = {-INFINITY, -INFINITY};
+  float m[NB][NCT];
+#pragma unroll
+  for (int br = 0; br < NB; ++br)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) m[br][ct] = -INFINITY;
 
+  // The next tile is loaded into registers while the current one is attended from LDS, then written to the
+  // other LDS stage; one barrier per tile.
   u32x4 rk[T::NCH], rkd[T::NCH], rv[T::NCH];
   auto gload = [&](int t) {
 #pragma unroll
     for (int j = 0; j < T::NCH; ++j) {
-      const int c = tid + 256 * j;
+      const int c = tid + T::NT * j;
       rk[j] = ld16(Kb + static_cast<int64_t>(t) * 64 * D + c * 8);
       rkd[j] = ld16(Kdb + static_cast<int64_t>(t) * 64 * D + c * 8);
-      rv[j] = ld16(Vb + static_cast<int64_t>(t) * D * 64 + c * 8);
+      rv[j] = ld16(Vb + static_cast<int64_t>(t) * 64 * D + c * 8);
     }
   };
   auto swrite = [&](int stage) {
     uint16_t* s = smem + stage * T::STAGE;
 #pragma unroll
     for (int j = 0; j < T::NCH; ++j) {
-      const int c = tid + 256 * j;
+      const int c = tid + T::NT * j;
       const int krow = c / (D / 8), kcol = (c % (D / 8)) * 8;
       *reinterpret_cast<u32x4*>(s + krow * T::KP + kcol) = rk[j];
       *reinterpret_cast<u32x4*>(s + T::K_ELEMS + krow * T::KP + kcol) = rkd[j];
-      const int vrow = c >> 3, vcol = (c & 7) * 8;
-      *reinterpret_cast<u32x4*>(s + 2 * T::K_ELEMS + vrow * T::VP + vcol) = rv[j];
+      *reinterpret_cast<u32x4*>(s + 2 * T::K_ELEMS + krow * T::KP + kcol) = rv[j];
     }
   };
+  auto attend = [&](int stage, bool masked, int kt0) {
+    const uint16_t* s = smem + stage * T::STAGE;
+    attend_tile<D, NB, NCT, FAST>([&](int b) { return s + (br0 + b) * T::K_ELEMS; }, s + 2 * T::K_ELEMS, T::KP,
+                                  T::KP, [&](int b, int ct, int kk) { return qf[b][ct][kk]; }, o, lsum, m, c,
+                                  masked, [&](int k, int) { return kt0 + k < L; });
+  };
 
+  // Full tiles run unmasked; the ragged last tile (keys >= L do not exist) is peeled off after the loop so the
+  // loop body has a single code path and the accumulators keep their registers.
+  const int nfull = L / 64;
   gload(0);
   swrite(0);
   __syncthreads();
-  for (int t = 0; t < nkt; ++t) {
+  for (int t = 0; t < nfull; ++t) {
     if (t + 1 < nkt) gload(t + 1);
-    const uint16_t* s = smem + (t & 1) * T::STAGE;
-    const int kt0 = t * 64;
-    if (kt0 + 64 > L)  // ragged last tile: keys >= L do not exist
-      attend_tile<D, FAST, true>(s, s + T::K_ELEMS, s + 2 * T::K_ELEMS, T::KP, T::VP, qf, o, lsum, m, c,
-                                 [&](int k) { return kt0 + k < L; });
-    else
-      attend_tile<D, FAST, false>(s, s + T::K_ELEMS, s + 2 * T::K_ELEMS, T::KP, T::VP, qf, o, lsum, m, c,
-                                  [](int) { return true; });
-
+    attend(t & 1, false, 0);
     if (t + 1 < nkt) swrite((t + 1) & 1);
     __syncthreads();
   }
+  if (nfull < nkt) attend(nfull & 1, true, nfull * 64);
 }
 
 template <int D>
-__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(const uint16_t* __restrict__ ws, int64_t region, int B,
-                                                            int L, int Lp, int H, const float* __restrict__ qw,
-                                                            const float* __restrict__ kw,
-                                                            const float* __restrict__ lam,
-                                                            uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
+    const uint16_t* __restrict__ ws, int64_t region, int B, int L, int Lp, int H, const float* __restrict__ qw,
+    const float* __restrict__ kw, const float* __restrict__ lam, uint16_t* __restrict__ out) {
   using T = DenseTile<D>;
+  constexpr int NB = T::NB, NCT = T::NCT;
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * T::STAGE];
   const int nqb = Lp / 128;
   const int tile = xcd_remap(blockIdx.x, B * H * nqb);
   const int qb = tile % nqb, bh = tile / nqb, h = bh % H, b = bh / H;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 31, lh = lane >> 5;
-  const int q0 = qb * 128 + wave * 32;
+  const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
+  const int br0 = T::SPLIT ? wave >> 1 : 0;                          // first branch of this wave
+  const int q0 = qb * 128 + (T::SPLIT ? (wave & 1) * 64 : wave * 32);  // first query of this wave
   const int64_t rowbase = static_cast<int64_t>(bh) * Lp;
 
   // Launch-uniform choice between the max-free and the running-max softmax (see the file comment).
   const SoftmaxPlan plan = dense_plan<D>(qw, kw);
 
-  u32x4 qf[2][D / 16];
+  u32x4 qf[NB][NCT][D / 16];
 #pragma unroll
-  for (int br = 0; br < 2; ++br)
+  for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
-      qf[br][kk] = ld16(ws + br * 2 * region + (rowbase + q0 + lr) * D + 16 * kk + 8 * lh);
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)  // q' is region 0, q_diff' region 2
+        qf[bi][ct][kk] = ld16(ws + (br0 + bi) * 2 * region + (rowbase + q0 + 32 * ct + lr) * D + 16 * kk + 8 * lh);
 
-  f32x16 o[2][D / 32];
+  f32x16 o[NB][NCT][D / 32];
+  float lsum[NB][NCT];
 #pragma unroll
-  for (int br = 0; br < 2; ++br)
+  for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt) o[br][dt] = f32x16{};
-  float lsum[2] = {0.f, 0.f};
+    for (int ct = 0; ct < NCT; ++ct) {
+      lsum[bi][ct] = 0.f;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) o[bi][ct][dt] = f32x16{};
+    }
 
   const uint16_t* Kb = ws + region + rowbase * D;
   const uint16_t* Kdb = ws + 3 * region + rowbase * D;
-  const uint16_t* Vb = ws + 4 * region + static_cast<int64_t>(bh) * (Lp / 64) * D * 64;
+  const uint16_t* Vb = ws + 4 * region + rowbase * D;
   if (plan.fast)
-    dense_attend_loop<D, true>(Kb, Kdb, Vb, L, smem, qf, o, lsum, plan.c);
+    dense_attend_loop<D, true>(Kb, Kdb, Vb, L, br0, smem, qf, o, lsum, plan.c);
   else
-    dense_attend_loop<D, false>(Kb, Kdb, Vb, L, smem, qf, o, lsum, plan.c);
+    dense_attend_loop<D, false>(Kb, Kdb, Vb, L, br0, smem, qf, o, lsum, plan.c);
 
-  const int q = q0 + lr;
-  uint16_t* orow = q < L ? out + (static_cast<int64_t>(b) * L + q) * (static_cast<int64_t>(H) * D) + h * D : nullptr;
-  store_diff_bf16<D>(orow, o, lsum, lam ? lam[h] : 1.f);
+  const float lamh = lam ? lam[h] : 1.f;
+  if constexpr (T::SPLIT) {
+    // Branch-2 waves publish lam * O2 / l2 (rounded per element); branch-1 waves subtract it from O1 / l1.
+    float* xbuf = reinterpret_cast<float*>(smem);  // 2 query halves x NCT x D/32 x 16 registers x 64 lanes
+    const int slot0 = (wave & 1) * NCT * (D / 32) * 16;
+    __syncthreads();  // every wave is done with the K / V tiles
+    if (br0 == 1) {
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const float i1 = __fmul_rn(lamh, inv_rowsum(lsum, 0, ct));
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            xbuf[(slot0 + (ct * (D / 32) + dt) * 16 + r) * 64 + lane] = __fmul_rn(o[0][ct][dt][r], i1);
+      }
+    }
+    __syncthreads();
+    if (br0 == 0) {
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const float i0 = inv_rowsum(lsum, 0, ct);
+        const int q = q0 + 32 * ct + lr;
+        uint16_t* orow = out + (static_cast<int64_t>(b) * L + q) * (static_cast<int64_t>(H) * D) + h * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * g + j;
+              v[j] = __fsub_rn(__fmul_rn(o[0][ct][dt][r], i0), xbuf[(slot0 + (ct * (D / 32) + dt) * 16 + r) * 64 + lane]);
+            }
+            if (q < L) {
+              u32x2 pk;
+              pk[0] = pack_bf16x2(v[0], v[1]);
+              pk[1] = pack_bf16x2(v[2], v[3]);
+              *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * lh) = pk;
+            }
+          }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      const int q = q0 + 32 * ct + lr;
+      uint16_t* orow = q < L ? out + (static_cast<int64_t>(b) * L + q) * (static_cast<int64_t>(H) * D) + h * D
+                             : nullptr;
+      store_diff_bf16<D, NCT>(orow, o, lsum, ct, lamh);
+    }
+  }
 }
 
 __global__ void rope_tables_kernel(const float* __restrict__ inv_freq, int half, int length, float* __restrict__ cosT,
@@ -365,10 +428,12 @@ extern "C" int hb_dense_attend(hipStream_t stream, const void* workspace, size_t
   uint16_t* o = static_cast<uint16_t*>(out);
   const int Lp = static_cast<int>(lay.Lp);
   if (D == 64)
-    hipLaunchKernelGGL(dense_attend_bf16<64>, dim3(nblocks), dim3(256), 0, stream, ws, lay.region_elems, B, L, Lp, H,
+    hipLaunchKernelGGL(dense_attend_bf16<64>, dim3(nblocks), dim3(DenseTile<64>::NT), 0, stream, ws, lay.region_elems,
+                       B, L, Lp, H,
                        q_weight, k_weight, lam, o);
   else
-    hipLaunchKernelGGL(dense_attend_bf16<128>, dim3(nblocks), dim3(256), 0, stream, ws, lay.region_elems, B, L, Lp, H,
+    hipLaunchKernelGGL(dense_attend_bf16<128>, dim3(nblocks), dim3(DenseTile<128>::NT), 0, stream, ws,
+                       lay.region_elems, B, L, Lp, H,
                        q_weight, k_weight, lam, o);
   return launch_status("dense_attend");
 }
