@@ -29,6 +29,9 @@ sys.path.insert(0, str(ROOT))
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+# HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes over `bench.py --kernels-only`
+# (written by hummingbird_amd.rocprof_summary); reported as roofline.traffic when present.
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_120s_clip.json"
 
 
 def parse() -> argparse.Namespace:
@@ -235,6 +238,11 @@ def main() -> int:
         # prep reads the 5 qkv sections and writes them back prepared: 2 x 5 H D bf16 per token
         "dense_prep": {"avg_us": round(prep_s * 1e6, 2), "gbs": round(2 * B * L * 5 * H * D * 2 / prep_s / 1e9, 1)},
     }
+    if TRAFFIC_FILE.exists():
+        measured = json.loads(TRAFFIC_FILE.read_text())["hbm_bytes_per_launch"]
+        for key, kernel in (("roofline", "dense_attend_bf16<64>"), ("roofline_band", "band_attend_bf16<64>")):
+            result[key]["traffic"] = measured.get(kernel)
+            result[key]["traffic_source"] = str(TRAFFIC_FILE.relative_to(ROOT))
     if not args.no_cpu and not args.kernels_only:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -1,0 +1,116 @@
+"""Turns rocprofv3 output of ``bench.py`` into the short text summaries kept with the measurements.
+
+Inputs are rocprofv3 output directories written with ``-o run --output-format csv``:
+
+  --trace DIR   a ``--kernel-trace --stats`` run   (reads run_kernel_stats.csv)
+  --fetch DIR   a ``--pmc FETCH_SIZE`` run          (reads run_counter_collection.csv)
+  --write DIR   a ``--pmc WRITE_SIZE`` run
+
+HBM traffic per launch is calibrated against the largest ``__amd_rocclr_copyBuffer`` dispatch of the same run,
+a device-to-device copy of ``--copy-bytes`` bytes (``bench.py --kernels-only`` issues one of 256 MiB): the copy
+reads and writes exactly that many bytes, so ``factor = bytes / counter`` converts each counter to bytes.
+
+Writes a markdown summary (``--md``) and, with ``--json``, the per-launch traffic that ``bench.py`` reports as
+``roofline.traffic``.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import json
+import re
+from pathlib import Path
+
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
+def short_name(name: str) -> str:
+    """``void hb::dense_attend_bf16<64>(...)`` -> ``dense_attend_bf16<64>``; other kernels keep a short prefix."""
+    m = re.search(r"hb::(\w+)(<\d+>)?", name)
+    if m:
+        return m.group(1) + (m.group(2) or "")
+    return name.split("(")[0][:60]
+
+
+def kernel_stats(trace_dir: Path) -> dict[str, dict]:
+    rows = {}
+    for r in csv.DictReader(open(trace_dir / "run_kernel_stats.csv")):
+        rows[short_name(r["Name"])] = {"calls": int(r["Calls"]), "avg_us": float(r["AverageNs"]) / 1e3,
+                                       "min_us": float(r["MinNs"]) / 1e3, "max_us": float(r["MaxNs"]) / 1e3,
+                                       "pct": float(r["Percentage"])}
+    return rows
+
+
+def counter(pmc_dir: Path, name: str) -> tuple[dict[str, float], float]:
+    """Average counter value per dispatch for each kernel, and the value of the largest copy dispatch."""
+    vals: dict[str, list[float]] = collections.defaultdict(list)
+    copy = 0.0
+    for r in csv.DictReader(open(pmc_dir / "run_counter_collection.csv")):
+        if r["Counter_Name"] != name:
+            continue
+        v = float(r["Counter_Value"])
+        k = short_name(r["Kernel_Name"])
+        vals[k].append(v)
+        if k == COPY_KERNEL:
+            copy = max(copy, v)
+    return {k: sum(v) / len(v) for k, v in vals.items()}, copy
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--trace", type=Path, required=True)
+    ap.add_argument("--fetch", type=Path)
+    ap.add_argument("--write", type=Path)
+    ap.add_argument("--copy-bytes", type=int, default=1 << 28)
+    ap.add_argument("--algorithmic", action="append", default=[], metavar="KERNEL=BYTES",
+                    help="algorithmic bytes per launch, for the traffic/algorithmic ratio")
+    ap.add_argument("--command", action="append", default=[], help="command lines to quote in the summary")
+    ap.add_argument("--title", default="rocprofv3 summary")
+    ap.add_argument("--md", type=Path, required=True)
+    ap.add_argument("--json", type=Path)
+    args = ap.parse_args()
+
+    stats = kernel_stats(args.trace)
+    algo = {k: float(v) for k, v in (a.split("=", 1) for a in args.algorithmic)}
+    lines = [f"# {args.title}", "", "Commands (from the repository root on the GPU host):", "", "```"]
+    lines += args.command + ["```", "", "## Kernel trace (`--kernel-trace --stats`)", "",
+                             "| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|"]
+    for k, s in sorted(stats.items(), key=lambda kv: -kv[1]["pct"]):
+        lines.append(f"| `{k}` | {s['calls']} | {s['avg_us']:.2f} | {s['min_us']:.2f} | {s['max_us']:.2f} "
+                     f"| {s['pct']:.2f} |")
+
+    traffic = {}
+    if args.fetch and args.write:
+        fetch, copy_fetch = counter(args.fetch, "FETCH_SIZE")
+        write, copy_write = counter(args.write, "WRITE_SIZE")
+        if copy_fetch <= 0 or copy_write <= 0:
+            raise SystemExit(f"no {COPY_KERNEL} dispatch found for calibration")
+        ff = args.copy_bytes / 1024 / copy_fetch
+        wf = args.copy_bytes / 1024 / copy_write
+        lines += ["", "## HBM traffic (`--pmc FETCH_SIZE`, `--pmc WRITE_SIZE`; KiB per dispatch)", "",
+                  f"Calibration: a {args.copy_bytes >> 20} MiB device copy reads FETCH_SIZE = {copy_fetch:.0f} KiB "
+                  f"and WRITE_SIZE = {copy_write:.0f} KiB, so bytes = FETCH_SIZE x {ff:.3f} x 1024 and "
+                  f"WRITE_SIZE x {wf:.3f} x 1024.", "",
+                  "| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes / launch | algorithmic bytes | ratio |",
+                  "|---|---|---|---|---|---|"]
+        for k in sorted(set(fetch) & set(write)):
+            if not k.startswith(("dense", "band", "rope")):
+                continue
+            total = (fetch[k] * ff + write[k] * wf) * 1024
+            traffic[k] = total
+            a = algo.get(k)
+            tail = f"{a:.4g} | {total / a:.2f} |" if a else "- | - |"
+            lines.append(f"| `{k}` | {fetch[k]:.0f} | {write[k]:.0f} | {total:.4g} | {tail}")
+    args.md.write_text("\n".join(lines) + "\n")
+    if args.json is not None:
+        args.json.write_text(json.dumps({"hbm_bytes_per_launch": {k: round(v) for k, v in traffic.items()},
+                                         "avg_us": {k: round(s["avg_us"], 2) for k, s in stats.items()
+                                                    if k.startswith(("dense", "band", "rope"))},
+                                         "commands": args.command}, indent=1) + "\n")
+    print(args.md.read_text())
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
