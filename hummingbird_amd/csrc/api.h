@@ -33,4 +33,14 @@ DenseLayout dense_layout(int dtype, int B, int L, int H, int D);
 
 int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int half);
 
+// fp32 kernels (fp32.hip). Arguments are validated by the exported entry points before these are called.
+int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qw, const float* kw,
+                          const float* cosT, const float* sinT, int half, const float* vmask, int B, int L, int H,
+                          int D, float eps, const DenseLayout& lay, void* ws);
+int launch_dense_attend_f32(hipStream_t stream, const void* ws, const float* lam, void* out, int B, int L, int H,
+                            int D, const DenseLayout& lay);
+int launch_band_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qdyt, const float* kdyt,
+                    const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
+                    int S, int H, int D);
+
 }  // namespace hb

@@ -335,11 +335,16 @@ extern "C" int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, 
   if (!qkv || !q_dyt || !k_dyt || !out) return fail(HB_ERR_NULL, "qkv, q_dyt, k_dyt and out must be non-NULL");
   if (half > 0 && (!cos || !sin)) return fail(HB_ERR_NULL, "cos and sin must be non-NULL when half > 0");
   if (half % 8 != 0) return fail(HB_ERR_HALF, "band kernel needs half %% 8 == 0 (half=%d)", half);
+  // A half-width of S or more reaches every key; clamping keeps the kernels' key-range arithmetic within int.
+  if (window > S) window = S;
   if (reinterpret_cast<uintptr_t>(qkv) % 16) return fail(HB_ERR_STRIDE, "qkv must be 16-byte aligned");
   if (half > 0 && (reinterpret_cast<uintptr_t>(cos) % 16 || reinterpret_cast<uintptr_t>(sin) % 16))
     return fail(HB_ERR_STRIDE, "cos and sin must be 16-byte aligned");
+  if (dtype == HB_F32) {
+    if (reinterpret_cast<uintptr_t>(out) % 16) return fail(HB_ERR_STRIDE, "fp32 out must be 16-byte aligned");
+    return launch_band_f32(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D);
+  }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
-  if (dtype != HB_BF16) return fail(HB_ERR_DTYPE, "band fp32 path not built yet");
   const int nblocks = B * H * ((S + BandCfg<64>::QB - 1) / BandCfg<64>::QB);
   const uint16_t* x = static_cast<const uint16_t*>(qkv);
   uint16_t* o = static_cast<uint16_t*>(out);

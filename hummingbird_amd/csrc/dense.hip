@@ -396,7 +396,9 @@ extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int
   if (half % 8 != 0) return fail(HB_ERR_HALF, "dense kernel needs half %% 8 == 0 (half=%d)", half);
   if (half > 0 && (reinterpret_cast<uintptr_t>(cos) % 16 || reinterpret_cast<uintptr_t>(sin) % 16))
     return fail(HB_ERR_STRIDE, "cos and sin must be 16-byte aligned");
-  if (dtype != HB_BF16) return fail(HB_ERR_DTYPE, "dense fp32 path not built yet");
+  if (dtype == HB_F32)
+    return launch_dense_prep_f32(stream, qkv, row_stride, q_weight, k_weight, cos, sin, half, vmask, B, L, H, D, eps,
+                                 lay, workspace);
   const dim3 grid(static_cast<unsigned>(lay.Lp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
   const uint16_t* x = static_cast<const uint16_t*>(qkv);
   uint16_t* ws = static_cast<uint16_t*>(workspace);
@@ -421,8 +423,11 @@ extern "C" int hb_dense_attend(hipStream_t stream, const void* workspace, size_t
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(HB_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (workspace_bytes < lay.total_bytes)
     return fail(HB_ERR_WORKSPACE, "workspace holds %zu bytes, needs %zu", workspace_bytes, lay.total_bytes);
+  if (dtype == HB_F32) {
+    if (reinterpret_cast<uintptr_t>(out) % 16) return fail(HB_ERR_STRIDE, "fp32 out must be 16-byte aligned");
+    return launch_dense_attend_f32(stream, workspace, lam, out, B, L, H, D, lay);
+  }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
-  if (dtype != HB_BF16) return fail(HB_ERR_DTYPE, "dense fp32 path not built yet");
   const int nblocks = B * H * static_cast<int>(lay.Lp / 128);
   const uint16_t* ws = static_cast<const uint16_t*>(workspace);
   uint16_t* o = static_cast<uint16_t*>(out);

@@ -97,14 +97,29 @@ def test_band_wide_window_equals_dense_attention():
     assert np.array_equal(a, b)
 
 
-def test_band_fp32_vs_oracle():
-    announce("band fp32 small")
-    inp = workloads.band_inputs(1, 300, 2, 64, 17, seed=6, dtype="fp32")
-    try:
-        got = run_hip(inp, dtype=torch.float32)
-    except TypeError as e:
-        pytest.skip(str(e))
-    assert_fp32_parity(got, oracle(inp, "xla", compute="fp32"), "fp32")
+FP32_SHAPES = [  # (B, S, H, D, window, half)
+    (1, 300, 2, 64, 17, 32), (1, 100, 2, 64, 0, 32), (2, 257, 2, 64, 64, 16), (1, 300, 2, 128, 17, 64),
+    (1, 50, 2, 64, 60, 0), (1, 1000, 1, 64, 128, 32),
+]
+
+
+@pytest.mark.parametrize("shape", FP32_SHAPES, ids=lambda s: "B%dS%dH%dD%dw%dh%d" % s)
+def test_band_fp32_vs_oracle(shape):
+    b, length, h, d, w, half = shape
+    announce(f"band fp32 {shape}")
+    inp = workloads.band_inputs(b, length, h, d, w, seed=6 + length, dtype="fp32", half=half)
+    got = run_hip(inp, dtype=torch.float32)
+    assert_fp32_parity(got, oracle(inp, "xla", compute="fp32"), f"fp32 {shape}")
+
+
+def test_band_fp32_identical_branches_cancel():
+    announce("band fp32 identical branches")
+    inp = workloads.band_inputs(1, 300, 2, 64, 40, seed=5, dtype="fp32")
+    qkv = inp["qkv"].copy()
+    hd = 2 * 64
+    qkv[..., 3 * hd:4 * hd] = qkv[..., 0:hd]
+    qkv[..., 4 * hd:5 * hd] = qkv[..., hd:2 * hd]
+    assert np.count_nonzero(run_hip(inp, dtype=torch.float32, lam=False, qkv_override=qkv)) == 0
 
 
 def test_band_120s_vs_torch_chain():

@@ -115,14 +115,37 @@ def test_dense_lambda_linearity():
     assert np.abs(ah - 0.5 * (a0 + a1)).max() <= 4e-3 * max(1.0, np.abs(a0).max())
 
 
-def test_dense_fp32_vs_oracle():
-    announce("dense fp32 small")
-    inp = workloads.dense_inputs(2, 150, 2, 64, seed=10, dtype="fp32")
-    try:
-        got = run_hip(inp, dtype=torch.float32)
-    except TypeError as e:  # fp32 kernel not built yet
-        pytest.skip(str(e))
-    assert_fp32_parity(got, oracle(inp, "xla", compute="fp32"), "fp32")
+FP32_SHAPES = [  # (B, L, H, D, half, ragged)
+    (2, 1, 2, 64, 32, False), (2, 150, 2, 64, 32, False), (2, 216, 4, 64, 16, True), (1, 300, 2, 64, 0, False),
+    (2, 129, 2, 128, 64, True), (1, 70, 3, 128, 32, False),
+]
+
+
+@pytest.mark.parametrize("shape", FP32_SHAPES, ids=lambda s: "B%dL%dH%dD%dh%d%s" % (*s[:5], "r" if s[5] else ""))
+def test_dense_fp32_vs_oracle(shape):
+    b, length, h, d, half, ragged = shape
+    announce(f"dense fp32 {shape}")
+    inp = workloads.dense_inputs(b, length, h, d, seed=10 + length, dtype="fp32", half=half, ragged=ragged,
+                                 mask_tail=min(16, length // 4))
+    got = run_hip(inp, dtype=torch.float32)
+    assert_fp32_parity(got, oracle(inp, "xla", compute="fp32"), f"fp32 {shape}")
+
+
+def test_dense_fp32_5s_clip():
+    """The 5 s clip shape with fp32 inputs: B=1, L=216, 24 heads of 64, rotary half 32, last 16 tokens masked."""
+    announce("dense fp32 B1 L216 H24 D64")
+    inp = workloads.dense_inputs(1, 216, 24, 64, seed=0, dtype="fp32", half=32, mask_tail=16)
+    got = run_hip(inp, dtype=torch.float32)
+    assert_fp32_parity(got, oracle(inp, "xla", compute="fp32"), "fp32 5 s clip")
+
+
+def test_dense_fp32_identical_branches_cancel():
+    announce("dense fp32 identical branches")
+    inp = workloads.dense_inputs(2, 100, 2, 64, seed=4, dtype="fp32")
+    x = inp["qkv"].reshape(2, 100, 5, 2 * 64).copy()
+    x[:, :, 3], x[:, :, 4] = x[:, :, 0], x[:, :, 1]
+    got = run_hip(inp, dtype=torch.float32, lam=False, qkv_override=x.reshape(2, 100, -1))
+    assert np.count_nonzero(got) == 0
 
 
 def test_dense_120s_vs_torch_chain():
