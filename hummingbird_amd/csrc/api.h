@@ -39,6 +39,12 @@ int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, const
                           int D, float eps, const DenseLayout& lay, void* ws);
 int launch_dense_attend_f32(hipStream_t stream, const void* ws, const float* lam, void* out, int B, int L, int H,
                             int D, const DenseLayout& lay);
+// Streaming band kernel (band_ring.hip): bf16, D = 64, half % 16 == 0, window <= 128. Arguments are validated by
+// hb_band_diffattn before the launch.
+bool band_ring_supported(int dtype, int D, int half, int window);
+int launch_band_ring(hipStream_t stream, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
+                     const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
+                     int S, int H);
 int launch_band_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qdyt, const float* kdyt,
                     const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                     int S, int H, int D);

@@ -345,6 +345,8 @@ extern "C" int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, 
     return launch_band_f32(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D);
   }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
+  if (band_ring_supported(dtype, D, half, window))
+    return launch_band_ring(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H);
   const int nblocks = B * H * ((S + BandCfg<64>::QB - 1) / BandCfg<64>::QB);
   const uint16_t* x = static_cast<const uint16_t*>(qkv);
   uint16_t* o = static_cast<uint16_t*>(out);

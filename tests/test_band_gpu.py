@@ -141,6 +141,37 @@ def test_band_120s_vs_torch_chain():
     assert_bf16_parity(got[0, -tail:, h * 64:(h + 1) * 64], ref_head[-tail:], "120s head 3 tail vs oracle")
 
 
+RUNS = [  # (B, S, H, window, half, gamma_mean): several 64-query steps per workgroup, runs crossing heads/batches
+    (2, 9000, 3, 128, 32, 1.0), (1, 20000, 2, 64, 16, 1.0), (2, 7001, 3, 17, 32, 1.0), (1, 18000, 1, 0, 32, 1.0),
+    (1, 16500, 2, 100, 8, 1.0), (1, 9000, 3, 128, 24, 1.0), (2, 8000, 2, 128, 32, 8.0),
+]
+
+
+@pytest.mark.parametrize("shape", RUNS, ids=lambda s: "B%dS%dH%dw%dh%dg%g" % s)
+def test_band_multistep_runs_vs_torch_chain(shape):
+    """Shapes with more 64-query steps than CUs, so each workgroup streams a run of steps and some runs cross a
+    (batch, head) boundary; checked against the torch restatement of the XLA chain, and the first and last
+    300 positions of the last head against the oracle (the sequence edges)."""
+    b, s, h, w, half, gm = shape
+    announce(f"band bf16 multistep {shape}")
+    inp = workloads.band_inputs(b, s, h, 64, w, seed=s + h + w, half=half, gamma_mean=gm)
+    got = run_hip(inp)
+    qkv = torch.from_numpy(inp["qkv"]).to(DEV, torch.bfloat16)
+    ref = xla_chain.band_chain(qkv, norm_t(inp["q_norm"]), norm_t(inp["k_norm"]),
+                               torch.from_numpy(inp["inv_freq"]).to(DEV), h, 64, w,
+                               lam=torch.from_numpy(inp["lam"]).to(DEV)).float().cpu().numpy()
+    if gm == 1.0:
+        assert_bf16_parity(got, ref, f"multistep {shape}")
+    else:  # logits reach ~50 here: the XLA chain keeps q/k in fp32, the fused cast points round them to bf16
+        assert stats(got, ref)["cosine"] >= 0.999, f"multistep {shape}: {stats(got, ref)}"
+    hh = h - 1
+    cols = np.concatenate([np.arange(sec * h * 64 + hh * 64, sec * h * 64 + hh * 64 + 64) for sec in range(5)])
+    head = dict(inp, qkv=np.ascontiguousarray(inp["qkv"][-1:, :, cols]), heads=1, lam=inp["lam"][hh:hh + 1])
+    exp = oracle(head, "xla" if gm == 1.0 else "fused")[0]
+    for lo, hi in ((0, 300), (s - 300, s)):
+        assert_bf16_parity(got[-1, lo:hi, hh * 64:(hh + 1) * 64], exp[lo:hi], f"multistep {shape} [{lo},{hi}) vs oracle")
+
+
 def test_band_errors_are_value_errors():
     announce("band argument errors")
     qkv = torch.zeros((1, 8, 5 * 2 * 64), device=DEV, dtype=torch.bfloat16)
