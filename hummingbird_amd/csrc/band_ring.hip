@@ -58,7 +58,7 @@ __device__ __forceinline__ float dyt(float x, float a2, float g2, float gb) {
 }
 
 // Raw inputs of one prep task: groups m1, m2 of tensors A and B (k and k_diff, or q and q_diff) of one row,
-// and the cos / sin slice of frequencies 8 m1 .. 8 m1 + 7 (1 and 0 when the pair is not rotated).
+// and the cos / sin slice of frequencies 8 m1 .. 8 m1 + 7 (unused when the pair is not rotated, or half = 0).
 struct Raw {
   u32x4 a1, a2, b1, b2;
   f32x4 c0, c1, s0, s1;
@@ -68,10 +68,16 @@ struct Prepped {
 };
 
 // DyT + RoPE (+ scale) of one task; A and B share the DyT parameters `par` = [-2 gamma (D) | gamma + beta (D)].
-__device__ __forceinline__ void prep_task(const Raw& r, int m1, int m2, float a2, const float* __restrict__ par,
-                                          float scale, Prepped& o) {
-  const float cs[8] = {r.c0[0], r.c0[1], r.c0[2], r.c0[3], r.c1[0], r.c1[1], r.c1[2], r.c1[3]};
-  const float sn[8] = {r.s0[0], r.s0[1], r.s0[2], r.s0[3], r.s1[0], r.s1[1], r.s1[2], r.s1[3]};
+// `rot`: the pair is rotated (otherwise cos 1, sin 0).
+__device__ __forceinline__ void prep_task(const Raw& r, int m1, int m2, bool rot, float a2,
+                                          const float* __restrict__ par, float scale, Prepped& o) {
+  float cs[8] = {r.c0[0], r.c0[1], r.c0[2], r.c0[3], r.c1[0], r.c1[1], r.c1[2], r.c1[3]};
+  float sn[8] = {r.s0[0], r.s0[1], r.s0[2], r.s0[3], r.s1[0], r.s1[1], r.s1[2], r.s1[3]};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    cs[j] = rot ? cs[j] : 1.f;
+    sn[j] = rot ? sn[j] : 0.f;
+  }
 #pragma unroll
   for (int tsr = 0; tsr < 2; ++tsr) {
     float x1[8], x2[8], o1[8], o2[8];
@@ -95,36 +101,32 @@ __device__ __forceinline__ void prep_task(const Raw& r, int m1, int m2, float a2
   }
 }
 
-// One ring tile for an attention wave: 32 queries, one branch. EDGE = false: every key of the tile is in the
-// band of every query. EDGE = true: 32-key half rt takes part if act_rt and is masked per score if msk_rt;
-// [lo, hi] are the keys (relative to the tile start, minus 4 lh) this lane's query may see.
-template <bool FAST, bool EDGE>
-__device__ __forceinline__ void tile_step(const uint16_t* __restrict__ sk, const uint16_t* __restrict__ sv,
-                                          const int (&koff)[4], const int (&voff)[2], const u32x4 (&qf)[4],
-                                          f32x16 (&o)[2], float& lsum, float& m, float c, bool act0, bool act1,
-                                          bool msk0, bool msk1, int lo, int hi) {
-  const bool act[2] = {EDGE ? act0 : true, EDGE ? act1 : true};
-  const bool msk[2] = {EDGE && msk0, EDGE && msk1};
-  f32x16 sc[2];
+// S^T of one ring tile for an attention wave: 64 keys x its 32 queries (both 32-key halves).
+__device__ __forceinline__ void qk(const uint16_t* __restrict__ sk, const int (&koff)[4], const u32x4 (&qf)[4],
+                                   f32x16 (&sc)[2]) {
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     sc[rt] = f32x16{};
-    if (act[rt]) {
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) sc[rt] = mfma_bf16_32x32x16(lds16(sk + rt * 32 * D + koff[kk]), qf[kk], sc[rt]);
-    }
+    for (int kk = 0; kk < 4; ++kk) sc[rt] = mfma_bf16_32x32x16(lds16(sk + rt * 32 * D + koff[kk]), qf[kk], sc[rt]);
   }
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    if (msk[rt]) {
-      const unsigned span = static_cast<unsigned>(hi - lo);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int kc = 32 * rt + 8 * (r >> 2) + (r & 3);
-        sc[rt][r] = static_cast<unsigned>(kc - lo) <= span ? sc[rt][r] : -INFINITY;
-      }
-    }
-  }
+}
+
+// Softmax and PV of one ring tile from its scores `sc` (read only, so the caller's score buffers keep their
+// registers). act_rt: 32-key half rt takes part; msk_rt: it is cut by the band edge or the sequence end and is
+// masked per score to the keys [lo, lo + span] (relative to the tile start, minus 4 lh) this lane's query may
+// see. Both flags are wave-uniform.
+template <bool FAST>
+__device__ __forceinline__ void soft_pv(const f32x16 (&sc)[2], const uint16_t* __restrict__ sv, const int (&voff)[2],
+                                        f32x16 (&o)[2], float& lsum, float& m, float c, bool act0, bool act1,
+                                        bool msk0, bool msk1, int lo, unsigned span) {
+  const bool act[2] = {act0, act1};
+  const bool msk[2] = {msk0, msk1};
+  // A masked-out score's probability is exp2(-inf) = 0.
+  auto score = [&](int rt, int r) {
+    const int kc = 32 * rt + 8 * (r >> 2) + (r & 3);
+    return msk[rt] && static_cast<unsigned>(kc - lo) > span ? -INFINITY : sc[rt][r];
+  };
   float mb = 0.f;
   if constexpr (!FAST) {
     float mt = -INFINITY;
@@ -132,7 +134,7 @@ __device__ __forceinline__ void tile_step(const uint16_t* __restrict__ sk, const
     for (int rt = 0; rt < 2; ++rt)
       if (act[rt]) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[rt][r]);
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, score(rt, r));
       }
     mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * c;
     const float mn = fmaxf(m, mt);
@@ -145,25 +147,33 @@ __device__ __forceinline__ void tile_step(const uint16_t* __restrict__ sk, const
     mb = mn == -INFINITY ? 0.f : mn;
   }
   u32x4 pb[2][2];  // [rt][16-key half]: 8 bf16 probabilities each
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    if (!act[rt]) continue;
+  // Masked and unmasked halves are separate code, so unmasked halves pay nothing for the band edges.
+  auto probs = [&](int rt, auto sval) {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
+        const float s0 = sval(8 * hh + 2 * j), s1 = sval(8 * hh + 2 * j + 1);
         float e0, e1;
         if constexpr (FAST) {
-          e0 = fast_exp2(sc[rt][8 * hh + 2 * j]);
-          e1 = fast_exp2(sc[rt][8 * hh + 2 * j + 1]);
+          e0 = fast_exp2(s0);
+          e1 = fast_exp2(s1);
         } else {
-          e0 = fast_exp2(__fmaf_rn(sc[rt][8 * hh + 2 * j], c, -mb));
-          e1 = fast_exp2(__fmaf_rn(sc[rt][8 * hh + 2 * j + 1], c, -mb));
+          e0 = fast_exp2(__fmaf_rn(s0, c, -mb));
+          e1 = fast_exp2(__fmaf_rn(s1, c, -mb));
         }
         const uint32_t p = pack_bf16x2(e0, e1);
         pb[rt][hh][j] = p;
         lsum = add_bf16_pair(p, lsum);
       }
+  };
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    if (!act[rt]) continue;
+    if (msk[rt])
+      probs(rt, [&](int r) { return score(rt, r); });
+    else
+      probs(rt, [&](int r) { return sc[rt][r]; });
   }
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -192,25 +202,161 @@ struct Args {
   uint16_t* out;
 };
 
-template <int C, bool FAST>
-__device__ __forceinline__ void run(const Args& a, uint16_t* ring, uint16_t* qbuf, float* xbuf, const float* qpar,
-                                    const float* kpar, float qa2, float ka2, const SoftmaxPlan& plan) {
+// The flattened (batch, head, step) range of this workgroup, walked as runs of consecutive steps of one
+// (batch, head). Both roles walk it identically and meet at the same barriers: one after each run's ring fill,
+// two per step.
+struct Range {
+  int64_t beg, end;
+  __device__ Range(const Args& a) {
+    const int64_t G = gridDim.x, gi = blockIdx.x;
+    beg = a.total * gi / G;
+    end = a.total * (gi + 1) / G;
+  }
+};
+
+// Raw rows of one step for a prep thread: its key task (k, k_diff), its two V chunks, its query task (q, q_diff).
+struct Stage {
+  Raw k, q;
+  u32x4 v[2];
+};
+
+// Prep waves (4-7): fill the ring at the start of each run, then prepare step j + 1 during step j from rows
+// loaded during step j - 1. The step loop is unrolled by two over stage buffers A and B, so a buffer is loaded
+// in one step and consumed in the next without being copied (a copy would wait for the loads to land).
+template <int C>
+__device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16_t* qbuf, const float* qpar,
+                                           const float* kpar, float qa2, float ka2, float qscale) {
   constexpr int RING = 2 * C + 1;
-  const int t = threadIdx.x, lane = t & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
-  const bool prep_role = wave >= 4;  // uniform per wave
-  const int S = a.S, H = a.H, w = a.w, half = a.half;
+  const int t = threadIdx.x;
+  const int S = a.S, H = a.H, half = a.half;
   const int64_t HD = static_cast<int64_t>(H) * D;
   const int h8 = half >> 3;
-  const int64_t G = gridDim.x, gi = blockIdx.x;
-  const int64_t f_beg = a.total * gi / G, f_end = a.total * (gi + 1) / G;
-
-  // Prep geometry (waves 4-7): task row pt / 4, RoPE group pair pt % 4; V chunks pt and pt + 256.
+  // Task row pt / 4, RoPE group pair pt % 4; V chunks pt and pt + 256.
   const int pt = t & 255, prow = pt >> 2, pp = pt & 3;
   int m1, m2;
   pair_groups(pp, h8, m1, m2);
   const bool prot = pp < h8;
-  // Attention geometry (waves 0-3): query half, branch, per-lane LDS fragment offsets.
+  const Range rg(a);
+
+  for (int64_t f = rg.beg; f < rg.end;) {
+    const int bh = static_cast<int>(f / a.NS);
+    const int j0 = static_cast<int>(f % a.NS);
+    const int j1 = static_cast<int>(rg.end - f < a.NS - j0 ? j0 + (rg.end - f) : a.NS);
+    const int b = bh / H, h = bh % H;
+    const uint16_t* xb = a.qkv + static_cast<int64_t>(b) * S * a.rs + h * D;
+
+    // Rows outside [0, S) are read from a clamped position: their keys are always masked, their V chunks are
+    // replaced by zeros when stored and their queries are never stored. The RoPE slice of a pair that is not
+    // rotated is read from column 0 and replaced by (1, 0) in prep_task. Nothing here depends on the loaded
+    // values, so nothing waits for them until they are used.
+    auto load_raw = [&](int pos, int sa, int sb) {
+      Raw r;
+      const int cp = pos < 0 ? 0 : (pos < S ? pos : S - 1);
+      const uint16_t* row = xb + static_cast<int64_t>(cp) * a.rs;
+      r.a1 = ld16(row + sa * HD + 8 * m1);
+      r.a2 = ld16(row + sa * HD + 8 * m2);
+      r.b1 = ld16(row + sb * HD + 8 * m1);
+      r.b2 = ld16(row + sb * HD + 8 * m2);
+      if (half > 0) {
+        const int64_t toff = static_cast<int64_t>(cp) * half + (prot ? 8 * m1 : 0);
+        r.c0 = *reinterpret_cast<const f32x4*>(a.cosT + toff);
+        r.c1 = *reinterpret_cast<const f32x4*>(a.cosT + toff + 4);
+        r.s0 = *reinterpret_cast<const f32x4*>(a.sinT + toff);
+        r.s1 = *reinterpret_cast<const f32x4*>(a.sinT + toff + 4);
+      } else {
+        r.c0 = r.c1 = f32x4{1.f, 1.f, 1.f, 1.f};
+        r.s0 = r.s1 = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+      return r;
+    };
+    // Step jj's rows: key tile jj + C and the queries of step jj.
+    auto load_stage = [&](int jj) {
+      Stage st;
+      const int kt = jj + C;
+      st.k = load_raw(KT * kt + prow, 1, 4);  // k, k_diff
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int ch = pt + 256 * u, vpos = KT * kt + (ch >> 3);
+        const int vc = vpos < 0 ? 0 : (vpos < S ? vpos : S - 1);
+        st.v[u] = ld16(xb + static_cast<int64_t>(vc) * a.rs + 2 * HD + 8 * (ch & 7));
+      }
+      st.q = load_raw(QT * jj + prow, 0, 3);  // q, q_diff
+      return st;
+    };
+    auto store_tile = [&](int kt, const Prepped& ko, const u32x4 (&v)[2]) {
+      uint16_t* base = ring + ((kt % RING + RING) % RING) * TILE;
+      *reinterpret_cast<u32x4*>(base + kofs(prow, m1)) = ko.a1;
+      *reinterpret_cast<u32x4*>(base + kofs(prow, m2)) = ko.a2;
+      *reinterpret_cast<u32x4*>(base + TE + kofs(prow, m1)) = ko.b1;
+      *reinterpret_cast<u32x4*>(base + TE + kofs(prow, m2)) = ko.b2;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int ch = pt + 256 * u, vpos = KT * kt + (ch >> 3);
+        const bool in = vpos >= 0 && vpos < S;
+        *reinterpret_cast<u32x4*>(base + 2 * TE + vofs(ch >> 3, ch & 7)) = in ? v[u] : u32x4{0u, 0u, 0u, 0u};
+      }
+    };
+    auto store_q = [&](const Prepped& qo) {
+      *reinterpret_cast<u32x4*>(qbuf + kofs(prow, m1)) = qo.a1;
+      *reinterpret_cast<u32x4*>(qbuf + kofs(prow, m2)) = qo.a2;
+      *reinterpret_cast<u32x4*>(qbuf + TE + kofs(prow, m1)) = qo.b1;
+      *reinterpret_cast<u32x4*>(qbuf + TE + kofs(prow, m2)) = qo.b2;
+    };
+
+    // Ring fill for step j0: tiles j0 - C .. j0 + C, and the queries of j0.
+    Prepped ko, qo;
+#pragma unroll 1
+    for (int i = 0; i < RING; ++i) {
+      const Stage st = load_stage(j0 - 2 * C + i);  // key tile j0 - C + i (its query rows are not used)
+      prep_task(st.k, m1, m2, prot, ka2, kpar, 1.f, ko);
+      store_tile(j0 - C + i, ko, st.v);
+      if (i == RING - 1) {
+        const Stage sq = load_stage(j0);
+        prep_task(sq.q, m1, m2, prot, qa2, qpar, qscale, qo);
+        store_q(qo);
+      }
+    }
+    // Loads beyond the run's last step read clamped rows and are never stored.
+    Stage A = load_stage(j0 + 1 < j1 ? j0 + 1 : j0);
+    __syncthreads();
+
+    // One step: prepare step jj + 1 from `cur`, load step jj + 2 into `nxt`, then store after the first barrier.
+    auto step = [&](int jj, const Stage& cur, Stage& nxt) {
+      const bool next = jj + 1 < j1;
+      prep_task(cur.k, m1, m2, prot, ka2, kpar, 1.f, ko);
+      prep_task(cur.q, m1, m2, prot, qa2, qpar, qscale, qo);
+      // The prepared values are only consumed by the stores after the barrier; pin their computation here, while
+      // the attention waves are still busy, instead of letting the compiler sink it past the barrier.
+      asm volatile("" ::"v"(ko.a1), "v"(ko.a2), "v"(ko.b1), "v"(ko.b2), "v"(qo.a1), "v"(qo.a2), "v"(qo.b1),
+                   "v"(qo.b2));
+      nxt = load_stage(jj + 2 < j1 ? jj + 2 : jj);
+      __syncthreads();  // the attention waves are done with the oldest tile and the query buffer
+      if (next) {
+        store_tile(jj + 1 + C, ko, cur.v);
+        store_q(qo);
+      }
+      __syncthreads();
+    };
+#pragma unroll 1
+    for (int j = j0; j < j1; j += 2) {
+      Stage B;
+      step(j, A, B);
+      if (j + 1 >= j1) break;
+      step(j + 1, B, A);
+    }
+    f += j1 - j0;
+  }
+}
+
+// Attention waves (0-3), wave = (query half, branch).
+template <int C, bool FAST>
+__device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16_t* qbuf, float* xbuf, float c) {
+  constexpr int RING = 2 * C + 1;
+  const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
+  const int S = a.S, H = a.H, w = a.w;
+  const int64_t HD = static_cast<int64_t>(H) * D;
   const int qhalf = wave & 1, br = (wave >> 1) & 1;
+  // Per-lane LDS fragment offsets.
   const int kswz = (lr & 7) ^ ((lr >> 3) & 1);
   int koff[4];
 #pragma unroll
@@ -222,170 +368,95 @@ __device__ __forceinline__ void run(const Args& a, uint16_t* ring, uint16_t* qbu
     const int col = 32 * dt + 16 * (grp & 1) + 4 * (mm & 3);
     voff[dt] = (4 * (grp >> 1) + (mm >> 2)) * D + 8 * ((col >> 3) ^ ((mm >> 2) << 1)) + (col & 7);
   }
+  const Range rg(a);
 
-  for (int64_t f = f_beg; f < f_end;) {
+  for (int64_t f = rg.beg; f < rg.end;) {
     const int bh = static_cast<int>(f / a.NS);
     const int j0 = static_cast<int>(f % a.NS);
-    const int j1 = static_cast<int>(f_end - f < a.NS - j0 ? j0 + (f_end - f) : a.NS);
+    const int j1 = static_cast<int>(rg.end - f < a.NS - j0 ? j0 + (rg.end - f) : a.NS);
     const int b = bh / H, h = bh % H;
-    const uint16_t* xb = a.qkv + static_cast<int64_t>(b) * S * a.rs + h * D;
-
-    // ---- prep role -------------------------------------------------------------------------------------
-    Raw kr, qr;
-    Prepped ko, qo;
-    u32x4 vr[2];
-    // Raw rows of key tile kt (this thread's task row, two V chunks) and of the queries of step jj. Rows
-    // outside [0, S) are read from a clamped position: their keys are always masked, their V chunks are
-    // replaced by zeros and their queries are never stored.
-    auto load_raw = [&](Raw& r, int pos, int sa, int sb) {
-      const int cp = pos < 0 ? 0 : (pos < S ? pos : S - 1);
-      const uint16_t* row = xb + static_cast<int64_t>(cp) * a.rs;
-      r.a1 = ld16(row + sa * HD + 8 * m1);
-      r.a2 = ld16(row + sa * HD + 8 * m2);
-      r.b1 = ld16(row + sb * HD + 8 * m1);
-      r.b2 = ld16(row + sb * HD + 8 * m2);
-      if (half > 0) {
-        const int64_t toff = static_cast<int64_t>(cp) * half + (prot ? 8 * m1 : 0);
-        const f32x4 one = {1.f, 1.f, 1.f, 1.f}, zero = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 c0 = *reinterpret_cast<const f32x4*>(a.cosT + toff);
-        const f32x4 c1 = *reinterpret_cast<const f32x4*>(a.cosT + toff + 4);
-        const f32x4 s0 = *reinterpret_cast<const f32x4*>(a.sinT + toff);
-        const f32x4 s1 = *reinterpret_cast<const f32x4*>(a.sinT + toff + 4);
-        r.c0 = prot ? c0 : one;
-        r.c1 = prot ? c1 : one;
-        r.s0 = prot ? s0 : zero;
-        r.s1 = prot ? s1 : zero;
-      } else {
-        r.c0 = r.c1 = f32x4{1.f, 1.f, 1.f, 1.f};
-        r.s0 = r.s1 = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    };
-    auto load_tile = [&](int kt) {
-      load_raw(kr, KT * kt + prow, 1, 4);  // k, k_diff
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int ch = pt + 256 * u, vpos = KT * kt + (ch >> 3);
-        const int vc = vpos < 0 ? 0 : (vpos < S ? vpos : S - 1);
-        const u32x4 v = ld16(xb + static_cast<int64_t>(vc) * a.rs + 2 * HD + 8 * (ch & 7));
-        vr[u] = vpos == vc ? v : u32x4{0u, 0u, 0u, 0u};
-      }
-    };
-    auto store_tile = [&](int kt) {
-      uint16_t* base = ring + ((kt % RING + RING) % RING) * TILE;
-      *reinterpret_cast<u32x4*>(base + kofs(prow, m1)) = ko.a1;
-      *reinterpret_cast<u32x4*>(base + kofs(prow, m2)) = ko.a2;
-      *reinterpret_cast<u32x4*>(base + TE + kofs(prow, m1)) = ko.b1;
-      *reinterpret_cast<u32x4*>(base + TE + kofs(prow, m2)) = ko.b2;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int ch = pt + 256 * u;
-        *reinterpret_cast<u32x4*>(base + 2 * TE + vofs(ch >> 3, ch & 7)) = vr[u];
-      }
-    };
-    auto store_q = [&]() {
-      *reinterpret_cast<u32x4*>(qbuf + kofs(prow, m1)) = qo.a1;
-      *reinterpret_cast<u32x4*>(qbuf + kofs(prow, m2)) = qo.a2;
-      *reinterpret_cast<u32x4*>(qbuf + TE + kofs(prow, m1)) = qo.b1;
-      *reinterpret_cast<u32x4*>(qbuf + TE + kofs(prow, m2)) = qo.b2;
-    };
-
-    // Fill the ring for step j0 (tiles j0 - C .. j0 + C) and the query buffer.
-    if (prep_role) {
-#pragma unroll 1
-      for (int i = 0; i < RING; ++i) {
-        load_tile(j0 - C + i);
-        prep_task(kr, m1, m2, ka2, kpar, 1.f, ko);
-        store_tile(j0 - C + i);
-      }
-      load_raw(qr, QT * j0 + prow, 0, 3);  // q, q_diff
-      prep_task(qr, m1, m2, qa2, qpar, plan.qscale, qo);
-      store_q();
-    }
-    __syncthreads();
+    const float lamh = a.lam ? a.lam[h] : 1.f;
+    __syncthreads();  // ring fill
 
 #pragma unroll 1
     for (int j = j0; j < j1; ++j) {
-      const bool next = j + 1 < j1;
-      if (prep_role) {
-        if (next) {
-          load_tile(j + 1 + C);
-          load_raw(qr, QT * (j + 1) + prow, 0, 3);
-          prep_task(kr, m1, m2, ka2, kpar, 1.f, ko);
-          prep_task(qr, m1, m2, qa2, qpar, plan.qscale, qo);
-        }
-        __syncthreads();  // the attention waves are done with the oldest tile and the query buffer
-        if (next) {
-          store_tile(j + 1 + C);
-          store_q();
-        }
-        __syncthreads();
-      } else {
-        // ---- attention role ----------------------------------------------------------------------------
-        u32x4 qf[4];
-        const uint16_t* qsrc = qbuf + br * TE + 32 * qhalf * D;
+      u32x4 qf[4];
+      const uint16_t* qsrc = qbuf + br * TE + 32 * qhalf * D;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) qf[kk] = lds16(qsrc + koff[kk]);
-        f32x16 o[2] = {f32x16{}, f32x16{}};
-        float lsum = 0.f, m = -INFINITY;
-        const int qa = QT * j + 32 * qhalf;  // this wave's first query
-        const int q = qa + lr;
-        const int ulo = qa - w > 0 ? qa - w : 0;  // union band of the wave's queries
-        const int uhi = qa + 31 + w < S - 1 ? qa + 31 + w : S - 1;
-        const int qlo = q - w > 0 ? q - w : 0;    // this lane's band
-        const int qhi = q + w < S - 1 ? q + w : S - 1;
+      for (int kk = 0; kk < 4; ++kk) qf[kk] = lds16(qsrc + koff[kk]);
+      f32x16 o[2] = {f32x16{}, f32x16{}};
+      float lsum = 0.f, m = -INFINITY;
+      const int qa = QT * j + 32 * qhalf;  // this wave's first query
+      const int q = qa + lr;
+      const int ulo = qa - w > 0 ? qa - w : 0;  // union band of the wave's queries
+      const int uhi = qa + 31 + w < S - 1 ? qa + 31 + w : S - 1;
+      const int qlo = q - w > 0 ? q - w : 0;    // this lane's band
+      const int qhi = q + w < S - 1 ? q + w : S - 1;
+      // The wave's tiles form one contiguous range of the ring; the scores of tile i + 1 are issued on the
+      // matrix core before the softmax of tile i, so the two overlap.
+      const int ilo = (ulo >> 6) - (j - C), ihi = (uhi >> 6) - (j - C);
+      auto tile_ptr = [&](int i) {
+        const int kt = j - C + i;
+        return ring + ((kt % RING + RING) % RING) * TILE;
+      };
+      auto finish = [&](int i, const f32x16 (&sc)[2]) {
+        const int kt0 = KT * (j - C + i);
+        bool act[2], full[2];
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const int k0 = kt0 + 32 * rt, k1 = k0 + 31;
+          act[rt] = k1 >= ulo && k0 <= uhi;
+          full[rt] = k0 >= qa + 31 - w && k1 <= qa + w && k0 >= 0 && k1 <= S - 1;
+        }
+        soft_pv<FAST>(sc, tile_ptr(i) + 2 * TE, voff, o, lsum, m, c, act[0], act[1], !full[0], !full[1],
+                      qlo - kt0 - 4 * lh, static_cast<unsigned>(qhi - qlo));
+      };
+      // The next tile's scores are always issued (the last tile's twice), so both score buffers stay in fixed
+      // registers across the loop.
+      f32x16 sa[2], sb[2];
+      qk(tile_ptr(ilo) + br * TE, koff, qf, sa);
 #pragma unroll 1
-        for (int i = 0; i < RING; ++i) {
-          const int kt = j - C + i, kt0 = KT * kt;
-          const uint16_t* base = ring + ((kt % RING + RING) % RING) * TILE;
-          bool act[2], full[2];
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt) {
-            const int k0 = kt0 + 32 * rt, k1 = k0 + 31;
-            act[rt] = k1 >= ulo && k0 <= uhi;
-            full[rt] = k0 >= qa + 31 - w && k1 <= qa + w && k0 >= 0 && k1 <= S - 1;
-          }
-          if (!act[0] && !act[1]) continue;
-          if (act[0] && act[1] && full[0] && full[1])
-            tile_step<FAST, false>(base + br * TE, base + 2 * TE, koff, voff, qf, o, lsum, m, plan.c, true, true,
-                                   false, false, 0, 0);
-          else
-            tile_step<FAST, true>(base + br * TE, base + 2 * TE, koff, voff, qf, o, lsum, m, plan.c, act[0],
-                                  act[1], act[0] && !full[0], act[1] && !full[1], qlo - kt0 - 4 * lh,
-                                  qhi - kt0 - 4 * lh);
-        }
-        // Branch 2 publishes lam * O2 / l2 (rounded per element); branch 1 subtracts it from O1 / l1.
-        const float inv = __frcp_rn(lsum + __shfl_xor(lsum, 32, kWave));
-        float* xs = xbuf + qhalf * (2 * 16 * 64);
-        if (br == 1) {
-          const float li = __fmul_rn(a.lam ? a.lam[h] : 1.f, inv);
-#pragma unroll
-          for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) xs[(dt * 16 + r) * 64 + lane] = __fmul_rn(o[dt][r], li);
-        }
-        __syncthreads();
-        if (br == 0) {
-          uint16_t* orow = a.out + (static_cast<int64_t>(b) * S + q) * HD + h * D;
-#pragma unroll
-          for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              float v[4];
-#pragma unroll
-              for (int jj = 0; jj < 4; ++jj) {
-                const int r = 4 * g + jj;
-                v[jj] = __fsub_rn(__fmul_rn(o[dt][r], inv), xs[(dt * 16 + r) * 64 + lane]);
-              }
-              if (q < S) {
-                u32x2 pk;
-                pk[0] = pack_bf16x2(v[0], v[1]);
-                pk[1] = pack_bf16x2(v[2], v[3]);
-                *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * lh) = pk;
-              }
-            }
-        }
-        __syncthreads();
+      for (int i = ilo;;) {
+        qk(tile_ptr(i + 1 <= ihi ? i + 1 : i) + br * TE, koff, qf, sb);
+        finish(i, sa);
+        if (++i > ihi) break;
+        qk(tile_ptr(i + 1 <= ihi ? i + 1 : i) + br * TE, koff, qf, sa);
+        finish(i, sb);
+        if (++i > ihi) break;
       }
+
+      // Branch 2 publishes lam * O2 / l2 (rounded per element); branch 1 subtracts it from O1 / l1.
+      const float inv = __frcp_rn(lsum + __shfl_xor(lsum, 32, kWave));
+      float* xs = xbuf + qhalf * (2 * 16 * 64);
+      if (br == 1) {
+        const float li = __fmul_rn(lamh, inv);
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) xs[(dt * 16 + r) * 64 + lane] = __fmul_rn(o[dt][r], li);
+      }
+      __syncthreads();
+      if (br == 0) {
+        uint16_t* orow = a.out + (static_cast<int64_t>(b) * S + q) * HD + h * D;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float v[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+              const int r = 4 * g + jj;
+              v[jj] = __fsub_rn(__fmul_rn(o[dt][r], inv), xs[(dt * 16 + r) * 64 + lane]);
+            }
+            if (q < S) {
+              u32x2 pk;
+              pk[0] = pack_bf16x2(v[0], v[1]);
+              pk[1] = pack_bf16x2(v[2], v[3]);
+              *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * lh) = pk;
+            }
+          }
+      }
+      __syncthreads();
     }
     f += j1 - j0;
   }
@@ -419,10 +490,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const SoftmaxPlan plan = softmax_plan(dyt_bound(a.q_dyt), dyt_bound(a.k_dyt), D);
   const float qa2 = 2.f * kLog2e * a.q_dyt[0], ka2 = 2.f * kLog2e * a.k_dyt[0];
   __syncthreads();
-  if (plan.fast)
-    run<C, true>(a, ring, qbuf, xbuf, par, par + 2 * D, qa2, ka2, plan);
+  if (wave_id() >= 4)
+    prep_waves<C>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
+  else if (plan.fast)
+    attn_waves<C, true>(a, ring, qbuf, xbuf, plan.c);
   else
-    run<C, false>(a, ring, qbuf, xbuf, par, par + 2 * D, qa2, ka2, plan);
+    attn_waves<C, false>(a, ring, qbuf, xbuf, plan.c);
 }
 
 }  // namespace band_ring
