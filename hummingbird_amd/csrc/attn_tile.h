@@ -69,17 +69,19 @@ __device__ __forceinline__ SoftmaxPlan softmax_plan(float qn, float kn, int D) {
 // `masked` (wave-uniform) only switches on the per-score masking step, so masked and unmasked tiles share
 // registers; `valid(key_in_tile, ct)` then decides whether a key takes part for column tile ct (false -> weight
 // 0). Branches run one after the other up to their probabilities, so only one branch's scores are live at a time.
-// `sk(b)` is the LDS K tile of branch slot b; `qf(b, ct, kk)` the B operand (8 bf16 of this lane's query in
-// column tile ct) for branch slot b and dims 16kk .. 16kk+15.
-template <int D, int NB, int NCT, bool FAST, class KTile, class QFrag, class Valid>
-__device__ __forceinline__ void attend_tile(KTile sk, const uint16_t* __restrict__ sV, int kp, int vp, QFrag qf,
-                                            f32x16 (&o)[NB][NCT][D / 32], float (&lsum)[NB][NCT],
-                                            float (&m)[NB][NCT], float c, bool masked, Valid valid) {
-  const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
+// `kf(b, rt, kk)` is the A operand of S^T for branch slot b: this lane's 8 bf16 of key row 32 rt + lr, dims
+// 16 kk + 8 lh .. +8. `vf(dt, g)` is the A operand of O^T: dim 32 dt + lr of the eight keys
+// {16 g + 8 (j / 4) + 4 lh + j % 4 : j < 8} that the lane's probability registers hold (see v_frag).
+// `qf(b, ct, kk)` is the B operand (8 bf16 of this lane's query in column tile ct) for branch slot b and dims
+// 16 kk + 8 lh .. +8.
+template <int D, int NB, int NCT, bool FAST, class KFrag, class VFrag, class QFrag, class Valid>
+__device__ __forceinline__ void attend_tile(KFrag kf, VFrag vf, QFrag qf, f32x16 (&o)[NB][NCT][D / 32],
+                                            float (&lsum)[NB][NCT], float (&m)[NB][NCT], float c, bool masked,
+                                            Valid valid) {
+  const int lane = threadIdx.x & 63, lh = lane >> 5;
   u32x4 pb[NB][NCT][2][2];  // [branch][column tile][row tile][16-key half]: 8 bf16 probabilities each
 #pragma unroll
   for (int br = 0; br < NB; ++br) {
-    const uint16_t* kt = sk(br);
     f32x16 sc[NCT][2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
@@ -88,7 +90,7 @@ __device__ __forceinline__ void attend_tile(KTile sk, const uint16_t* __restrict
       for (int ct = 0; ct < NCT; ++ct) acc[ct] = f32x16{};
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
-        const u32x4 a = lds16(kt + (32 * rt + lr) * kp + 16 * kk + 8 * lh);
+        const u32x4 a = kf(br, rt, kk);
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) acc[ct] = mfma_bf16_32x32x16(a, qf(br, ct, kk), acc[ct]);
       }
@@ -146,7 +148,7 @@ __device__ __forceinline__ void attend_tile(KTile sk, const uint16_t* __restrict
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const u32x4 a = v_frag(sV, vp, dt, g);
+      const u32x4 a = vf(dt, g);
 #pragma unroll
       for (int br = 0; br < NB; ++br)
 #pragma unroll

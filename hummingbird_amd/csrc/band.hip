@@ -226,8 +226,11 @@ __device__ __forceinline__ void band_loop(const uint16_t* __restrict__ xb, int64
     const int klast = kt0 + C::KT - 1;
     if (kt0 <= qa + 31 + window && klast >= qa - window) {
       const bool inside = kt0 >= qa + 31 - window && klast <= qa + window && klast < S;
-      attend_tile<D, 2, 1, FAST>([&](int br) { return s + br * C::K_ELEMS; }, s + 2 * C::K_ELEMS, C::KP, C::KP,
-                                 qf, o, lsum, m, c, !inside, [&](int k, int) {
+      const int klh = (threadIdx.x >> 5) & 1;
+      attend_tile<D, 2, 1, FAST>(
+          [&](int br, int rt, int kk) { return lds16(s + br * C::K_ELEMS + (32 * rt + lr) * C::KP + 16 * kk + 8 * klh); },
+          [&](int dt, int g) { return v_frag(s + 2 * C::K_ELEMS, C::KP, dt, g); }, qf, o, lsum, m, c, !inside,
+          [&](int k, int) {
                              const int key = kt0 + k, dist = key - q;
                              return (key < S) & (dist <= window) & (dist >= -window);
                            });

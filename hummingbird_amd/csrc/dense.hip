@@ -24,6 +24,32 @@
 
 namespace hb {
 
+// Layout of a prepared 64-key V tile: transposed, V^T[d][pos], with the keys of every 16-key group in the order
+// that the probability registers of a lane hold them. Lane half lh of the PV MFMA takes the keys
+// {16 g + 8 (j / 4) + 4 lh + j % 4 : j < 8}; storing key 16 g + 8 a + 4 b + c at position 16 g + 8 b + 4 a + c
+// (bits 2 and 3 swapped, an involution) puts them at the eight consecutive positions 16 g + 8 lh .. +8.
+__device__ __forceinline__ int v_tile_key(int pos) { return (pos & ~12) | ((pos & 4) << 1) | ((pos & 8) >> 1); }
+
+// Asynchronous 16-byte copy global -> LDS for a whole wave: lane i's 16 bytes at `sbase` + `voff` bytes
+// (`sbase` wave-uniform) land at byte 16 i of the 1 KB LDS block `dst` (wave-uniform). Issued as inline assembly
+// so that the compiler does not serialise it against the LDS reads of the other stage; the caller waits for it
+// (s_waitcnt vmcnt(0)) before the barrier that publishes the stage.
+__device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint16_t* dst) {
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) uint16_t*)dst));
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(__builtin_amdgcn_readfirstlane(lds)),
+               "v"(voff), "s"(sbase)
+               : "m0");
+}
+
+// XOR swizzle of the 16-byte chunks of an LDS row of RL elements, so that the MFMA operand reads (one chunk of
+// 16 consecutive rows per cycle) hit distinct banks.
+template <int RL>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  if constexpr (RL == 64) return row * 64 + 8 * (chunk ^ (row & 7) ^ ((row >> 3) & 1));
+  else return row * RL + 8 * (chunk ^ (row & 15));
+}
+
 // After RMSNorm a row has |x| <= sqrt(D) * max|w|, so the plan depends only on the two gain vectors; the prep
 // and attention kernels evaluate it identically.
 template <int D>
@@ -153,7 +179,9 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     }
   }
 
-  // V * mask, row-major like k (the attention kernel reads it with transposing LDS loads).
+  // V * mask, transposed per 64-key tile (v_tile_pos): the attention kernel then reads its PV operand with
+  // full-rate 16-byte LDS loads instead of transposing ones. The tile is staged in LDS row-major first.
+  __shared__ __attribute__((aligned(16))) uint16_t vt[64 * D];
 #pragma unroll
   for (int i = 0; i < VCH; ++i) {
     const int ch = t + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8;
@@ -161,7 +189,19 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     unpack8(vraw[i], x);
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] *= vm[i];
-    st16(ws + 4 * region + (bh * Lp + l0 + key) * D + col, pack8(x));
+    *reinterpret_cast<u32x4*>(vt + key * D + col) = pack8(x);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < VCH; ++i) {
+    const int ch = t + 256 * i, d = ch / 8, pos0 = (ch % 8) * 8;
+    uint16_t e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = vt[v_tile_key(pos0 + j) * D + d];
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(e[2 * j]) | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
+    st16(ws + 4 * region + (bh * Lp + l0) * D + d * 64 + pos0, w);
   }
 }
 
@@ -176,15 +216,16 @@ struct DenseTile {
   static constexpr int NB = SPLIT ? 1 : 2;  // branches per wave
   static constexpr int NCT = SPLIT ? 2 : 1; // 32-query column tiles per wave
   static constexpr int NT = 256;            // threads per workgroup
-  static constexpr int KP = D + 8;          // K, K_diff and V row pitch in elements (144 B for D = 64)
-  static constexpr int K_ELEMS = 64 * KP;
-  static constexpr int STAGE = 3 * K_ELEMS; // K, K_diff, V of one 64-key tile, all row-major
-  static constexpr int NCH = 64 * D / 8 / NT;  // 16-byte chunks per thread per 64-key tile of one tensor
+  static constexpr int K_ELEMS = 64 * D;     // one tensor of a 64-key tile: K, K_diff [key][d]; V^T [d][pos]
+  static constexpr int STAGE = 3 * K_ELEMS;  // K, K_diff, V^T of one 64-key tile, swizzled rows
+  static constexpr int BPT = 64 * D * 2 / 1024;  // 1 KB blocks per tensor of a 64-key tile
+  static constexpr int NBLK = 3 * BPT;            // blocks per tile (a multiple of the 4 waves)
 };
 
 template <int D, bool FAST>
 __device__ __forceinline__ void dense_attend_loop(const uint16_t* __restrict__ Kb, const uint16_t* __restrict__ Kdb,
-                                                  const uint16_t* __restrict__ Vb, int L, int br0, uint16_t* smem,
+                                                  const uint16_t* __restrict__ Vb, int L, int br0, uint16_t* sA,
+                                                  uint16_t* sB,
                                                   const u32x4 (&qf)[DenseTile<D>::NB][DenseTile<D>::NCT][D / 16],
                                                   f32x16 (&o)[DenseTile<D>::NB][DenseTile<D>::NCT][D / 32],
                                                   float (&lsum)[DenseTile<D>::NB][DenseTile<D>::NCT], float c) {
@@ -198,49 +239,64 @@ __device__ __forceinline__ void dense_attend_loop(const uint16_t* __restrict__ K
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) m[br][ct] = -INFINITY;
 
-  // The next tile is loaded into registers while the current one is attended from LDS, then written to the
-  // other LDS stage; one barrier per tile.
-  u32x4 rk[T::NCH], rkd[T::NCH], rv[T::NCH];
-  auto gload = [&](int t) {
+  // The next tile is copied from the workspace straight into the other LDS stage (global_load_lds, no
+  // registers) while the current one is attended; one wait and one barrier per tile. Each wave copies 1 KB
+  // blocks: lane i lands at byte 16 i of its block, so it fetches the chunk that the swizzled layout puts there.
+  const int wv = tid >> 6, ln = tid & 63;
+  // Byte offset of this lane's chunk inside its wave's 1 KB block; the same for every block of a tensor, since
+  // the swizzle depends on the row only through bits the block index does not change.
+  const int r64 = ln >> 3;                                   // rows of 64 elements: 8 per block
+  const uint32_t off64 = static_cast<uint32_t>(wv * 1024 + r64 * 128 + 16 * ((ln & 7) ^ (r64 & 7) ^ (wv & 1)));
+  const int r128 = ln >> 4;                                  // rows of 128 elements: 4 per block
+  const uint32_t off128 = static_cast<uint32_t>(wv * 1024 + r128 * 256 + 16 * ((ln & 15) ^ (4 * (wv & 3) + r128)));
+  auto issue = [&](int t, uint16_t* s) {
 #pragma unroll
-    for (int j = 0; j < T::NCH; ++j) {
-      const int c = tid + T::NT * j;
-      rk[j] = ld16(Kb + static_cast<int64_t>(t) * 64 * D + c * 8);
-      rkd[j] = ld16(Kdb + static_cast<int64_t>(t) * 64 * D + c * 8);
-      rv[j] = ld16(Vb + static_cast<int64_t>(t) * 64 * D + c * 8);
+    for (int tsr = 0; tsr < 3; ++tsr) {  // K, K_diff [key][d]; V^T [d][pos]
+      const uint16_t* base = (tsr == 0 ? Kb : tsr == 1 ? Kdb : Vb) + static_cast<int64_t>(t) * 64 * D;
+      const uint32_t off = tsr < 2 && D == 128 ? off128 : off64;
+#pragma unroll
+      for (int u = 0; u < T::BPT / 4; ++u)  // blocks wv, wv + 4, ...
+        lds_dma16(base, off + u * 4096, s + tsr * T::K_ELEMS + (wv + 4 * u) * 512);
     }
   };
-  auto swrite = [&](int stage) {
-    uint16_t* s = smem + stage * T::STAGE;
-#pragma unroll
-    for (int j = 0; j < T::NCH; ++j) {
-      const int c = tid + T::NT * j;
-      const int krow = c / (D / 8), kcol = (c % (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(s + krow * T::KP + kcol) = rk[j];
-      *reinterpret_cast<u32x4*>(s + T::K_ELEMS + krow * T::KP + kcol) = rkd[j];
-      *reinterpret_cast<u32x4*>(s + 2 * T::K_ELEMS + krow * T::KP + kcol) = rv[j];
-    }
-  };
-  auto attend = [&](int stage, bool masked, int kt0) {
-    const uint16_t* s = smem + stage * T::STAGE;
-    attend_tile<D, NB, NCT, FAST>([&](int b) { return s + (br0 + b) * T::K_ELEMS; }, s + 2 * T::K_ELEMS, T::KP,
-                                  T::KP, [&](int b, int ct, int kk) { return qf[b][ct][kk]; }, o, lsum, m, c,
-                                  masked, [&](int k, int) { return kt0 + k < L; });
+  const int lr = tid & 31, lh = (tid >> 5) & 1;
+  auto attend = [&](const uint16_t* s, bool masked, int kt0) {
+    attend_tile<D, NB, NCT, FAST>(
+        [&](int b, int rt, int kk) { return lds16(s + (br0 + b) * T::K_ELEMS + swz<D>(32 * rt + lr, 2 * kk + lh)); },
+        [&](int dt, int g) { return lds16(s + 2 * T::K_ELEMS + swz<64>(32 * dt + lr, 2 * g + lh)); },
+        [&](int b, int ct, int kk) { return qf[b][ct][kk]; }, o, lsum, m, c, masked,
+        [&](int k, int) { return kt0 + k < L; });
   };
 
   // Full tiles run unmasked; the ragged last tile (keys >= L do not exist) is peeled off after the loop so the
   // loop body has a single code path and the accumulators keep their registers.
+  // The two stages are separate LDS arrays and the loop is unrolled over them, so the compiler can see that a
+  // tile's reads never touch the stage being filled and does not wait for the copy before reading.
+  // A copy has landed once this wave's vector-memory counter drains (s_waitcnt 0); the barrier then publishes
+  // every wave's copies.
   const int nfull = L / 64;
-  gload(0);
-  swrite(0);
+  issue(0, sA);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int t = 0; t < nfull; ++t) {
-    if (t + 1 < nkt) gload(t + 1);
-    attend(t & 1, false, 0);
-    if (t + 1 < nkt) swrite((t + 1) & 1);
+  int t = 0;
+  for (; t + 1 < nfull; t += 2) {
+    issue(t + 1, sB);  // stage B was last read in tile t - 1
+    attend(sA, false, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < nkt) issue(t + 2, sA);
+    attend(sB, false, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  if (nfull < nkt) attend(nfull & 1, true, nfull * 64);
+  if (t < nfull) {  // an odd number of full tiles: the last one sits in stage A
+    if (t + 1 < nkt) issue(t + 1, sB);
+    attend(sA, false, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    ++t;
+  }
+  if (nfull < nkt) attend((nfull & 1) ? sB : sA, true, nfull * 64);  // the ragged last tile
 }
 
 template <int D>
@@ -249,7 +305,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
     const float* __restrict__ kw, const float* __restrict__ lam, uint16_t* __restrict__ out) {
   using T = DenseTile<D>;
   constexpr int NB = T::NB, NCT = T::NCT;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * T::STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t smem[T::STAGE];   // stage A (also the epilogue's exchange)
+  __shared__ __attribute__((aligned(16))) uint16_t smemB[T::STAGE];  // stage B
   const int nqb = Lp / 128;
   const int tile = xcd_remap(blockIdx.x, B * H * nqb);
   const int qb = tile % nqb, bh = tile / nqb, h = bh % H, b = bh / H;
@@ -285,9 +342,9 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
   const uint16_t* Kdb = ws + 3 * region + rowbase * D;
   const uint16_t* Vb = ws + 4 * region + rowbase * D;
   if (plan.fast)
-    dense_attend_loop<D, true>(Kb, Kdb, Vb, L, br0, smem, qf, o, lsum, plan.c);
+    dense_attend_loop<D, true>(Kb, Kdb, Vb, L, br0, smem, smemB, qf, o, lsum, plan.c);
   else
-    dense_attend_loop<D, false>(Kb, Kdb, Vb, L, br0, smem, qf, o, lsum, plan.c);
+    dense_attend_loop<D, false>(Kb, Kdb, Vb, L, br0, smem, smemB, qf, o, lsum, plan.c);
 
   const float lamh = lam ? lam[h] : 1.f;
   if constexpr (T::SPLIT) {
