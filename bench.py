@@ -32,6 +32,9 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
 # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE passes over `bench.py --kernels-only`
 # (written by hummingbird_amd.rocprof_summary); reported as roofline.traffic when present.
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_120s_clip.json"
+# Kernels that the two calls launch at these shapes (D = 64; window 128 takes the two-tile ring variant).
+DENSE_KERNEL = "dense_attend_bf16<64>"
+BAND_KERNEL = "band_ring_bf16<2>"
 
 
 def parse() -> argparse.Namespace:
@@ -161,6 +164,8 @@ def main() -> int:
             band_call()
 
     if args.kernels_only:
+        for _ in range(args.warmup):  # clocks settle as in the timed run
+            step()
         src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
         dst.copy_(src)  # 256 MiB read + 256 MiB written: calibrates FETCH_SIZE / WRITE_SIZE
@@ -229,18 +234,18 @@ def main() -> int:
                    "host_wall_s": round(host_s, 3)},
         "roofline": {"bound": "mfma", "achieved": round(attend_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(attend_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "dense_attend_bf16<64>", "avg_us": round(attend_s * 1e6, 2),
+                     "kernel": DENSE_KERNEL, "avg_us": round(attend_s * 1e6, 2),
                      "flops_per_launch": dense_fl},
         "roofline_band": {"bound": "hbm", "achieved": round(band_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(band_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                          "kernel": "band_attend_bf16<64>", "avg_us": round(band_s * 1e6, 2),
+                          "kernel": BAND_KERNEL, "avg_us": round(band_s * 1e6, 2),
                           "bytes_per_launch": band_by, "tflops": round(band_fl / band_s / 1e12, 1)},
         # prep reads the 5 qkv sections and writes them back prepared: 2 x 5 H D bf16 per token
         "dense_prep": {"avg_us": round(prep_s * 1e6, 2), "gbs": round(2 * B * L * 5 * H * D * 2 / prep_s / 1e9, 1)},
     }
     if TRAFFIC_FILE.exists():
         measured = json.loads(TRAFFIC_FILE.read_text())["hbm_bytes_per_launch"]
-        for key, kernel in (("roofline", "dense_attend_bf16<64>"), ("roofline_band", "band_attend_bf16<64>")):
+        for key, kernel in (("roofline", DENSE_KERNEL), ("roofline_band", BAND_KERNEL)):
             result[key]["traffic"] = measured.get(kernel)
             result[key]["traffic_source"] = str(TRAFFIC_FILE.relative_to(ROOT))
     if not args.no_cpu and not args.kernels_only:
