@@ -270,8 +270,7 @@ __device__ __forceinline__ void dense_attend_loop(const uint16_t* __restrict__ K
 
   // Full tiles run unmasked; the ragged last tile (keys >= L do not exist) is peeled off after the loop so the
   // loop body has a single code path and the accumulators keep their registers.
-  // The two stages are separate LDS arrays and the loop is unrolled over them, so the compiler can see that a
-  // tile's reads never touch the stage being filled and does not wait for the copy before reading.
+  // The loop is unrolled over the two stages so that both stage addresses are fixed in each half.
   // A copy has landed once this wave's vector-memory counter drains (s_waitcnt 0); the barrier then publishes
   // every wave's copies.
   const int nfull = L / 64;
@@ -305,8 +304,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
     const float* __restrict__ kw, const float* __restrict__ lam, uint16_t* __restrict__ out) {
   using T = DenseTile<D>;
   constexpr int NB = T::NB, NCT = T::NCT;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[T::STAGE];   // stage A (also the epilogue's exchange)
-  __shared__ __attribute__((aligned(16))) uint16_t smemB[T::STAGE];  // stage B
+  // Stages A and B of the K/V tiles; the epilogue reuses the first 32 KB as its exchange buffer.
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * T::STAGE];
   const int nqb = Lp / 128;
   const int tile = xcd_remap(blockIdx.x, B * H * nqb);
   const int qb = tile % nqb, bh = tile / nqb, h = bh % H, b = bh / H;
@@ -342,14 +341,15 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
   const uint16_t* Kdb = ws + 3 * region + rowbase * D;
   const uint16_t* Vb = ws + 4 * region + rowbase * D;
   if (plan.fast)
-    dense_attend_loop<D, true>(Kb, Kdb, Vb, L, br0, smem, smemB, qf, o, lsum, plan.c);
+    dense_attend_loop<D, true>(Kb, Kdb, Vb, L, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
   else
-    dense_attend_loop<D, false>(Kb, Kdb, Vb, L, br0, smem, smemB, qf, o, lsum, plan.c);
+    dense_attend_loop<D, false>(Kb, Kdb, Vb, L, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
 
   const float lamh = lam ? lam[h] : 1.f;
   if constexpr (T::SPLIT) {
     // Branch-2 waves publish lam * O2 / l2 (rounded per element); branch-1 waves subtract it from O1 / l1.
     float* xbuf = reinterpret_cast<float*>(smem);  // 2 query halves x NCT x D/32 x 16 registers x 64 lanes
+    static_assert(2 * NCT * (D / 32) * 16 * 64 * 4 <= 2 * T::STAGE * 2, "exchange buffer exceeds the two stages");
     const int slot0 = (wave & 1) * NCT * (D / 32) * 16;
     __syncthreads();  // every wave is done with the K / V tiles
     if (br0 == 1) {
