@@ -45,6 +45,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-iters", type=int, default=50, help="launches per live kernel timing")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the per-call timings at the reference-true and 380 s shapes")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel timing loops plus one 256 MiB device copy (the traffic-counter "
                          "calibration kernel); for profiling under rocprofv3")
@@ -93,6 +95,80 @@ def cpu_baseline(target_s: float) -> dict:
                        f"pairs at L={d['length']} x{n_dense}, {dense_call_s * 1e3:.0f} ms/call scaled; band 1 of "
                        f"{b['heads']} heads over {frames} of {b['length']} frames x{n_band}, "
                        f"{band_call_s * 1e3:.0f} ms/call scaled; host cpus={len(os.sched_getaffinity(0))}")}
+
+
+def call_percentiles(fn, n: int, stream) -> dict:
+    """Per-call duration percentiles (us) from HIP events around each of `n` warm calls on `stream`."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    ev[0].record(stream)
+    for i in range(n):
+        fn()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    us = np.array([ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(n)])
+    return {"p10": round(float(np.percentile(us, 10)), 2), "p50": round(float(np.median(us)), 2),
+            "p90": round(float(np.percentile(us, 90)), 2)}
+
+
+# Extra shapes, timed per call (not part of the clip value):
+#   reference-true 120 s geometry: DiT B=1, L=1422, 24 heads, rotary half 16; SAME-L S=23086, 24 heads, w=17
+#   380 s clip: DiT B=2, L=8180; SAME-L S=261760, 8 heads, w=128
+EXTRA_DENSE = {"ref_true_120s": (1, 1422, 24, 64, 16), "clip_380s": (2, 8180, 24, 64, 32)}
+EXTRA_BAND = {"ref_true_120s": (1, 23086, 24, 64, 17, 16), "clip_380s": (1, 261760, 8, 64, 128, 32)}
+
+
+def extra_shapes(lib, sp, stream, dev) -> dict:
+    """Per-call p10/p50/p90 and roofline fractions of the dense and band calls at the extra shapes (synthetic
+    N(0,1) qkv drawn on the device, unit gains, lam = 1)."""
+    import torch
+
+    from hummingbird_amd import _lib
+    from hummingbird_amd import band_attention as ba
+    from hummingbird_amd import dense_attention as da
+    from hummingbird_amd import workloads as wl
+
+    gen = torch.Generator(device=dev).manual_seed(7)
+    res = {}
+    for name, (B, L, H, D, half) in EXTRA_DENSE.items():
+        qkv = torch.randn((B, L, 5 * H * D), device=dev, generator=gen).to(torch.bfloat16)
+        ones = torch.ones(D, device=dev)
+        cos, sin, mask = da.tables(L, torch.from_numpy(wl.inv_freq(half)).to(dev), torch.ones((B, L), device=dev),
+                                   D, torch.bfloat16)
+        wsb = int(lib.hb_dense_workspace_size(_lib.HB_BF16, B, L, H, D))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        out = torch.empty((B, L, H * D), dtype=torch.bfloat16, device=dev)
+
+        def call():
+            _lib.check(lib.hb_dense_diffattn(sp, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, ones.data_ptr(),
+                                             ones.data_ptr(), cos.data_ptr(), sin.data_ptr(), half, mask.data_ptr(),
+                                             0, out.data_ptr(), B, L, H, D, 1e-6, ws.data_ptr(), wsb), "dense")
+        pc = call_percentiles(call, 20, stream)
+        tf = wl.dense_flops(B, L, H, D) / (pc["p50"] * 1e-6) / 1e12
+        res[f"dense_{name}"] = {"shape": {"B": B, "L": L, "H": H, "D": D, "half": half}, "us_per_call": pc,
+                                "tflops_p50": round(tf, 1), "mfma_frac_p50": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del qkv, ws, out
+    for name, (B, S, H, D, W, half) in EXTRA_BAND.items():
+        qkv = torch.randn((B, S, 5 * H * D), device=dev, generator=gen).to(torch.bfloat16)
+        dyt = {"alpha": torch.tensor(0.5), "gamma": torch.ones(D), "beta": torch.zeros(D)}
+        qd, kd = ba.pack_dyt(dyt, D, dev), ba.pack_dyt(dyt, D, dev)
+        cos, sin = ba.rope_tables(S, torch.from_numpy(wl.inv_freq(half)).to(dev))
+        out = torch.empty((B, S, H * D), dtype=torch.bfloat16, device=dev)
+
+        def bcall():
+            _lib.check(lib.hb_band_diffattn(sp, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, qd.data_ptr(), kd.data_ptr(),
+                                            cos.data_ptr(), sin.data_ptr(), half, W, 0, out.data_ptr(), B, S, H, D),
+                       "band")
+        pc = call_percentiles(bcall, 10, stream)
+        gbs = wl.band_bytes(B, S, H, D) / (pc["p50"] * 1e-6) / 1e9
+        res[f"band_{name}"] = {"shape": {"B": B, "S": S, "H": H, "D": D, "w": W, "half": half}, "us_per_call": pc,
+                               "gbs_p50": round(gbs, 1), "hbm_frac_p50": round(gbs / HBM_PEAK_GBS, 4),
+                               "tflops_p50": round(wl.band_flops(B, S, H, D, W) / (pc["p50"] * 1e-6) / 1e12, 1)}
+        del qkv, out
+    return res
 
 
 def main() -> int:
@@ -209,6 +285,8 @@ def main() -> int:
                                                         sin_d.data_ptr(), half_d, mask_d.data_ptr(), B, L, H, D, 1e-6,
                                                         ws.data_ptr(), ws_bytes), "prep"), args.kernel_iters)
     band_s = timed(band_call, max(5, args.kernel_iters // 5))
+    dense_pc = call_percentiles(lambda: dense_call(0), args.kernel_iters, stream)
+    band_pc = call_percentiles(band_call, max(5, args.kernel_iters // 5), stream)
     dense_fl, dense_by = wl.dense_flops(B, L, H, D), wl.dense_bytes(B, L, H, D)
     band_fl, band_by = wl.band_flops(1, S, HB, DB, W), wl.band_bytes(1, S, HB, DB)
     attend_tf = dense_fl / attend_s / 1e12
@@ -231,6 +309,7 @@ def main() -> int:
                                "band diff-attn (B=1, S=82688, H=8, D=64, w=128)",
                    "dense_ms_per_call": round((attend_s + prep_s) * 1e3, 4),
                    "band_ms_per_call": round(band_s * 1e3, 4),
+                   "dense_call_us": dense_pc, "band_call_us": band_pc,
                    "host_wall_s": round(host_s, 3)},
         "roofline": {"bound": "mfma", "achieved": round(attend_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(attend_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
@@ -248,6 +327,9 @@ def main() -> int:
         for key, kernel in (("roofline", DENSE_KERNEL), ("roofline_band", BAND_KERNEL)):
             result[key]["traffic"] = measured.get(kernel)
             result[key]["traffic_source"] = str(TRAFFIC_FILE.relative_to(ROOT))
+    if not args.no_extras and not args.kernels_only:
+        print("[bench] extra shapes", file=sys.stderr, flush=True)
+        result["extra_shapes"] = extra_shapes(lib, sp, stream, dev)
     if not args.no_cpu and not args.kernels_only:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
