@@ -45,6 +45,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-iters", type=int, default=50, help="launches per live kernel timing")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    ap.add_argument("--sweep", action="store_true",
+                    help="instead of the clip benchmark: the mixed-shape sweep (DiT L in {216, 1292, 2584} x "
+                         "D in {64, 128}, SAME-L S=16384 with w in {64, 128, 256}; bf16 and fp32), one JSON line "
+                         "per shape with its timing, roofline fraction and parity against the torch XLA chain")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the per-call timings at the reference-true and 380 s shapes")
     ap.add_argument("--kernels-only", action="store_true",
@@ -171,6 +175,90 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
     return res
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+
+
+def parity(got, ref, dtype: str) -> dict:
+    """max-abs, cosine and relative error against the torch restatement of the XLA chain, and whether they are
+    within the contract (bf16: max-abs <= 2e-2 and cosine >= 0.9999; fp32: <= 1e-5 relative)."""
+    g, r = got.double().flatten(), ref.double().flatten()
+    err = (g - r).abs().max().item()
+    cos = (g @ r / (g.norm() * r.norm())).item()
+    rel = err / max(r.abs().max().item(), 1e-30)
+    ok = (err <= 2e-2 and cos >= 0.9999) if dtype == "bf16" else rel <= 1e-5
+    return {"max_abs": float(f"{err:.3g}"), "cosine": round(cos, 7), "rel": float(f"{rel:.3g}"), "within_tolerance": ok}
+
+
+def sweep(lib, sp, stream, dev) -> None:
+    """Mixed-shape sweep: per shape, p50 per-call time, roofline fraction and parity (one JSON line each).
+    Dense: B=2, H = 1536 / D, ragged value mask (0-25 % tail per row). Band: B=1, S=16384, 8 heads of 64."""
+    import torch
+
+    from hummingbird_amd import _lib
+    from hummingbird_amd import band_attention as ba
+    from hummingbird_amd import dense_attention as da
+    from hummingbird_amd import workloads as wl
+    from hummingbird_amd import xla_chain
+
+    tdt = {"bf16": torch.bfloat16, "fp32": torch.float32}
+    for length in (216, 1292, 2584):
+        for D in (64, 128):
+            for dt in ("bf16", "fp32"):
+                B, H = 2, 1536 // D
+                inp = wl.dense_inputs(B, length, H, D, seed=length + D, dtype=dt, ragged=True)
+                qkv = torch.from_numpy(inp["qkv"]).to(dev, tdt[dt])
+                qw, kw = torch.from_numpy(inp["q_weight"]).to(dev), torch.from_numpy(inp["k_weight"]).to(dev)
+                lam, freq = torch.from_numpy(inp["lam"]).to(dev), torch.from_numpy(inp["inv_freq"]).to(dev)
+                valid = torch.from_numpy(inp["valid"]).to(dev)
+                cos, sin, mask = da.tables(length, freq, valid, D, tdt[dt])
+                code = _lib.HB_BF16 if dt == "bf16" else _lib.HB_F32
+                wsb = int(lib.hb_dense_workspace_size(code, B, length, H, D))
+                ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+                out = torch.empty((B, length, H * D), dtype=tdt[dt], device=dev)
+
+                def call():  # the C ABI directly, so host-side checks do not show up as GPU idle time
+                    _lib.check(lib.hb_dense_diffattn(sp, qkv.data_ptr(), code, 5 * H * D, qw.data_ptr(), kw.data_ptr(),
+                                                     cos.data_ptr(), sin.data_ptr(), inp["half"], mask.data_ptr(),
+                                                     lam.data_ptr(), out.data_ptr(), B, length, H, D, inp["eps"],
+                                                     ws.data_ptr(), wsb), "dense")
+                pc = call_percentiles(call, 20, stream)
+                ref = xla_chain.dense_chain(qkv, qw, kw, freq, valid, H, D, inp["eps"], lam=lam)
+                tf = wl.dense_flops(B, length, H, D) / (pc["p50"] * 1e-6) / 1e12
+                peak = MFMA_BF16_PEAK_TFLOPS if dt == "bf16" else FP32_MFMA_PEAK_TFLOPS
+                print(json.dumps({"sweep": "dense", "B": B, "L": length, "H": H, "D": D, "dtype": dt,
+                                  "us_per_call": pc, "tflops_p50": round(tf, 1), "peak_tflops": peak,
+                                  "peak_frac_p50": round(tf / peak, 4), **parity(out.float(), ref.float(), dt)}),
+                      flush=True)
+                del qkv, ws, out, ref
+    for w in (64, 128, 256):
+        for dt in ("bf16", "fp32"):
+            S, H, D = 16384, 8, 64
+            inp = wl.band_inputs(1, S, H, D, w, seed=w, dtype=dt)
+            qkv = torch.from_numpy(inp["qkv"]).to(dev, tdt[dt])
+            qn = {k: torch.as_tensor(np.asarray(v)).to(dev) for k, v in inp["q_norm"].items()}
+            kn = {k: torch.as_tensor(np.asarray(v)).to(dev) for k, v in inp["k_norm"].items()}
+            lam, freq = torch.from_numpy(inp["lam"]).to(dev), torch.from_numpy(inp["inv_freq"]).to(dev)
+            cos, sin = ba.rope_tables(S, freq)
+            qd, kd = ba.pack_dyt(qn, D, dev), ba.pack_dyt(kn, D, dev)
+            code = _lib.HB_BF16 if dt == "bf16" else _lib.HB_F32
+            out = torch.empty((1, S, H * D), dtype=tdt[dt], device=dev)
+
+            def call():
+                _lib.check(lib.hb_band_diffattn(sp, qkv.data_ptr(), code, 5 * H * D, qd.data_ptr(), kd.data_ptr(),
+                                                cos.data_ptr(), sin.data_ptr(), inp["half"], w, lam.data_ptr(),
+                                                out.data_ptr(), 1, S, H, D), "band")
+            pc = call_percentiles(call, 10, stream)
+            ref = xla_chain.band_chain(qkv, qn, kn, freq, H, D, w, lam=lam)
+            elem = 2 if dt == "bf16" else 4
+            gbs = wl.band_bytes(1, S, H, D, elem) / (pc["p50"] * 1e-6) / 1e9
+            print(json.dumps({"sweep": "band", "B": 1, "S": S, "H": H, "D": D, "w": w, "window": 2 * w,
+                              "dtype": dt, "us_per_call": pc, "gbs_p50": round(gbs, 1),
+                              "hbm_frac_p50": round(gbs / HBM_PEAK_GBS, 4),
+                              "tflops_p50": round(wl.band_flops(1, S, H, D, w) / (pc["p50"] * 1e-6) / 1e12, 1),
+                              **parity(out.float(), ref.float(), dt)}), flush=True)
+            del qkv, out, ref
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -190,6 +278,9 @@ def main() -> int:
     lib = _lib.load()
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
+    if args.sweep:
+        sweep(lib, sp, stream, dev)
+        return 0
 
     # ---- dense inputs (two qkv buffers alternate, as consecutive blocks would) ----
     d = wl.DENSE_120S

@@ -5,6 +5,7 @@ Inputs are rocprofv3 output directories written with ``-o run --output-format cs
   --trace DIR   a ``--kernel-trace --stats`` run   (reads run_kernel_stats.csv)
   --fetch DIR   a ``--pmc FETCH_SIZE`` run          (reads run_counter_collection.csv)
   --write DIR   a ``--pmc WRITE_SIZE`` run
+  --pmc DIR     any other ``--pmc`` run (repeatable), e.g. matrix-core busy cycles and LDS bank conflicts
 
 HBM traffic per launch is calibrated against the largest ``__amd_rocclr_copyBuffer`` dispatch of the same run,
 a device-to-device copy of ``--copy-bytes`` bytes (``bench.py --kernels-only`` issues one of 256 MiB): the copy
@@ -58,11 +59,61 @@ def counter(pmc_dir: Path, name: str) -> tuple[dict[str, float], float]:
     return {k: sum(v) / len(v) for k, v in vals.items()}, copy
 
 
+def all_counters(pmc_dir: Path) -> dict[str, dict[str, float]]:
+    """Average value per dispatch of every counter in a `--pmc` run, per kernel on the path."""
+    vals: dict[tuple[str, str], list[float]] = collections.defaultdict(list)
+    for r in csv.DictReader(open(pmc_dir / "run_counter_collection.csv")):
+        k = short_name(r["Kernel_Name"])
+        if k.startswith(("dense", "band")):
+            vals[(k, r["Counter_Name"])].append(float(r["Counter_Value"]))
+    out: dict[str, dict[str, float]] = collections.defaultdict(dict)
+    for (k, c), v in vals.items():
+        out[k][c] = sum(v) / len(v)
+    return out
+
+
+def agent(pmc_dir: Path) -> dict[str, int]:
+    for r in csv.DictReader(open(pmc_dir / "run_agent_info.csv")):
+        if r.get("Agent_Type") == "GPU":
+            return {k: int(r[k]) for k in ("Simd_Count", "Num_Xcc", "Cu_Count")}
+    raise SystemExit("no GPU agent in run_agent_info.csv")
+
+
+def counter_section(dirs: list[Path]) -> list[str]:
+    """Markdown table of the hardware counters of one or more `--pmc` passes, with the derived fractions:
+    matrix-core busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE / XCDs) (GRBM_GUI_ACTIVE is summed
+    over the XCDs, the busy cycles over the SIMDs), and LDS bank-conflict cycles per LDS-active cycle."""
+    merged: dict[str, dict[str, float]] = collections.defaultdict(dict)
+    info = agent(dirs[0])
+    for d in dirs:
+        for k, cs in all_counters(d).items():
+            merged[k].update(cs)
+    names = sorted({c for cs in merged.values() for c in cs})
+    lines = ["", "## Hardware counters (`--pmc`; average per dispatch, summed over the GPU)", "",
+             f"GPU: {info['Cu_Count']} CUs, {info['Simd_Count']} SIMDs, {info['Num_Xcc']} XCDs.", "",
+             "| kernel | " + " | ".join(names) + " | MFMA busy | LDS bank conflict / LDS active |",
+             "|---|" + "---|" * (len(names) + 2)]
+    for k in sorted(merged):
+        cs = merged[k]
+        busy = "-"
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in cs and cs.get("GRBM_GUI_ACTIVE"):
+            cycles = cs["GRBM_GUI_ACTIVE"] / info["Num_Xcc"]
+            busy = f"{cs['SQ_VALU_MFMA_BUSY_CYCLES'] / (info['Simd_Count'] * cycles):.1%}"
+        conf = "-"
+        if cs.get("SQ_LDS_IDX_ACTIVE") and "SQ_LDS_BANK_CONFLICT" in cs:
+            conf = f"{cs['SQ_LDS_BANK_CONFLICT'] / cs['SQ_LDS_IDX_ACTIVE']:.1%}"
+        lines.append(f"| `{k}` | " + " | ".join(f"{cs[c]:.4g}" if c in cs else "-" for c in names)
+                     + f" | {busy} | {conf} |")
+    return lines
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--trace", type=Path, required=True)
     ap.add_argument("--fetch", type=Path)
     ap.add_argument("--write", type=Path)
+    ap.add_argument("--pmc", type=Path, action="append", default=[],
+                    help="a --pmc run with other counters (repeatable); tabulated with derived fractions")
     ap.add_argument("--copy-bytes", type=int, default=1 << 28)
     ap.add_argument("--algorithmic", action="append", default=[], metavar="KERNEL=BYTES",
                     help="algorithmic bytes per launch, for the traffic/algorithmic ratio")
@@ -103,6 +154,8 @@ def main() -> int:
             a = algo.get(k)
             tail = f"{a:.4g} | {total / a:.2f} |" if a else "- | - |"
             lines.append(f"| `{k}` | {fetch[k]:.0f} | {write[k]:.0f} | {total:.4g} | {tail}")
+    if args.pmc:
+        lines += counter_section(args.pmc)
     args.md.write_text("\n".join(lines) + "\n")
     if args.json is not None:
         args.json.write_text(json.dumps({"hbm_bytes_per_launch": {k: round(v) for k, v in traffic.items()},
