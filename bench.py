@@ -49,6 +49,9 @@ def parse() -> argparse.Namespace:
                     help="instead of the clip benchmark: the mixed-shape sweep (DiT L in {216, 1292, 2584} x "
                          "D in {64, 128}, SAME-L S=16384 with w in {64, 128, 256}; bf16 and fp32), one JSON line "
                          "per shape with its timing, roofline fraction and parity against the torch XLA chain")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="instead of the clip benchmark: the data dependence of the matrix cores -- torch bf16 "
+                         "GEMMs (8192^3) and the dense call with N(0,1), all-zero and all-one inputs")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the per-call timings at the reference-true and 380 s shapes")
     ap.add_argument("--kernels-only", action="store_true",
@@ -259,6 +262,47 @@ def sweep(lib, sp, stream, dev) -> None:
             del qkv, out, ref
 
 
+def ceiling(lib, sp, stream, dev) -> None:
+    """Throughput of the matrix cores as a function of the operand data: the vendor GEMM (torch -> hipBLASLt,
+    bf16 8192^3) and the dense call at B=2, L=2584, H=24, D=64, each with N(0,1), all-zero and all-one inputs.
+    One JSON line per case."""
+    import torch
+
+    from hummingbird_amd import _lib
+    from hummingbird_amd import dense_attention as da
+    from hummingbird_amd import workloads as wl
+
+    n = 8192
+    for kind in ("randn", "zeros", "ones"):
+        a = getattr(torch, kind)((n, n), device=dev, dtype=torch.bfloat16)
+        b = getattr(torch, kind)((n, n), device=dev, dtype=torch.bfloat16)
+        pc = call_percentiles(lambda: torch.mm(a, b), 20, stream)
+        print(json.dumps({"ceiling": "torch.mm bf16", "shape": [n, n, n], "data": kind, "us_per_call": pc,
+                          "tflops_p50": round(2 * n ** 3 / (pc["p50"] * 1e-6) / 1e12, 1)}), flush=True)
+        del a, b
+    d = wl.DENSE_120S
+    B, L, H, D = d["batch"], d["length"], d["heads"], d["head_dim"]
+    inp = wl.dense_inputs(B, L, H, D, seed=0)
+    qw, kw = torch.from_numpy(inp["q_weight"]).to(dev), torch.from_numpy(inp["k_weight"]).to(dev)
+    cos, sin, mask = da.tables(L, torch.from_numpy(inp["inv_freq"]).to(dev), torch.from_numpy(inp["valid"]).to(dev),
+                               D, torch.bfloat16)
+    wsb = int(lib.hb_dense_workspace_size(_lib.HB_BF16, B, L, H, D))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    out = torch.empty((B, L, H * D), dtype=torch.bfloat16, device=dev)
+    for kind in ("randn", "zeros", "ones"):
+        qkv = getattr(torch, kind)((B, L, 5 * H * D), device=dev, dtype=torch.bfloat16)
+        _lib.check(lib.hb_dense_prep(sp, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, qw.data_ptr(), kw.data_ptr(),
+                                     cos.data_ptr(), sin.data_ptr(), inp["half"], mask.data_ptr(), B, L, H, D, 1e-6,
+                                     ws.data_ptr(), wsb), "prep")
+        pc = call_percentiles(lambda: _lib.check(lib.hb_dense_attend(sp, ws.data_ptr(), wsb, _lib.HB_BF16,
+                                                                     qw.data_ptr(), kw.data_ptr(), 0, out.data_ptr(),
+                                                                     B, L, H, D), "attend"), 50, stream)
+        print(json.dumps({"ceiling": DENSE_KERNEL, "shape": [B, L, H, D], "data": kind, "us_per_call": pc,
+                          "tflops_p50": round(wl.dense_flops(B, L, H, D) / (pc["p50"] * 1e-6) / 1e12, 1)}),
+              flush=True)
+        del qkv
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -280,6 +324,9 @@ def main() -> int:
     sp = stream.cuda_stream
     if args.sweep:
         sweep(lib, sp, stream, dev)
+        return 0
+    if args.ceiling:
+        ceiling(lib, sp, stream, dev)
         return 0
 
     # ---- dense inputs (two qkv buffers alternate, as consecutive blocks would) ----

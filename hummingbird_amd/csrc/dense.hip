@@ -179,9 +179,12 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     }
   }
 
-  // V * mask, transposed per 64-key tile (v_tile_pos): the attention kernel then reads its PV operand with
-  // full-rate 16-byte LDS loads instead of transposing ones. The tile is staged in LDS row-major first.
+  // V * mask, transposed per 64-key tile (v_tile_key order): the attention kernel then reads its PV operand
+  // with full-rate 16-byte LDS loads instead of transposing ones. The tile is staged in LDS row-major first, with
+  // the 16-byte chunks of row r XOR-swizzled by (r / 8) % 8: the column reads below take one dim of 8 rows that
+  // are 8 apart, which then fall in 8 different chunks (distinct banks) instead of one.
   __shared__ __attribute__((aligned(16))) uint16_t vt[64 * D];
+  auto vt_at = [](int row, int col) { return row * D + 8 * ((col >> 3) ^ ((row >> 3) & 7)) + (col & 7); };
 #pragma unroll
   for (int i = 0; i < VCH; ++i) {
     const int ch = t + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8;
@@ -189,7 +192,7 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     unpack8(vraw[i], x);
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] *= vm[i];
-    *reinterpret_cast<u32x4*>(vt + key * D + col) = pack8(x);
+    *reinterpret_cast<u32x4*>(vt + vt_at(key, col)) = pack8(x);
   }
   __syncthreads();
 #pragma unroll
@@ -197,7 +200,7 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     const int ch = t + 256 * i, d = ch / 8, pos0 = (ch % 8) * 8;
     uint16_t e[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) e[j] = vt[v_tile_key(pos0 + j) * D + d];
+    for (int j = 0; j < 8; ++j) e[j] = vt[vt_at(v_tile_key(pos0 + j), d)];
     u32x4 w;
 #pragma unroll
     for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(e[2 * j]) | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
