@@ -33,8 +33,8 @@ SIGNATURES = {
                                   c_size_t]),
     "hb_dense_prep": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                               c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t]),
-    "hb_dense_attend": (c_int, [c_void_p, c_void_p, c_size_t, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
-                                c_int, c_int, c_int]),
+    "hb_dense_attend": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t]),
     "hb_band_validate": (c_int, [c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_int]),
     "hb_band_diffattn": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                  c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int]),

@@ -27,7 +27,7 @@ DenseLayout dense_layout(int dtype, int B, int L, int H, int D) {
   lay.region_elems = static_cast<int64_t>(B) * H * lay.Lp * D;
   lay.elem_bytes = dtype == HB_F32 ? 4 : 2;
   lay.region_bytes = static_cast<size_t>(lay.region_elems) * lay.elem_bytes;
-  lay.total_bytes = 5 * lay.region_bytes;
+  lay.total_bytes = 3 * lay.region_bytes;
   return lay;
 }
 

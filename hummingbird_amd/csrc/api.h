@@ -19,9 +19,9 @@ constexpr int kDenseKeyTile = 64;
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-// The dense workspace holds five equally sized (B, H, Lp, D) regions of prepared (normalised, rotated or
-// masked) rows, Lp = L rounded up to kDenseQueryBlock and zero-filled past L. Elements are bf16
-// for HB_BF16 and fp32 for HB_F32. Region order: q', k', q_diff', k_diff', v'.
+// The dense workspace holds three equally sized (B, H, Lp, D) regions of prepared key-side rows, Lp = L rounded
+// up to kDenseQueryBlock and zero-filled past L: k' and k_diff' (normalised and rotated) and v' (V * mask).
+// Elements are bf16 for HB_BF16 and fp32 for HB_F32. The queries are prepared inside the attention kernel.
 struct DenseLayout {
   int64_t Lp;
   int64_t region_elems;  // B * H * Lp * D
@@ -34,11 +34,12 @@ DenseLayout dense_layout(int dtype, int B, int L, int H, int D);
 int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int half);
 
 // fp32 kernels (fp32.hip). Arguments are validated by the exported entry points before these are called.
-int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qw, const float* kw,
-                          const float* cosT, const float* sinT, int half, const float* vmask, int B, int L, int H,
-                          int D, float eps, const DenseLayout& lay, void* ws);
-int launch_dense_attend_f32(hipStream_t stream, const void* ws, const float* lam, void* out, int B, int L, int H,
-                            int D, const DenseLayout& lay);
+int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* kw, const float* cosT,
+                          const float* sinT, int half, const float* vmask, int B, int L, int H, int D, float eps,
+                          const DenseLayout& lay, void* ws);
+int launch_dense_attend_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qw, const float* cosT,
+                            const float* sinT, int half, float eps, const void* ws, const float* lam, void* out, int B,
+                            int L, int H, int D, const DenseLayout& lay);
 // Streaming band kernel (band_ring.hip): bf16, D = 64, half % 16 == 0, window <= 128. Arguments are validated by
 // hb_band_diffattn before the launch.
 bool band_ring_supported(int dtype, int D, int half, int window);

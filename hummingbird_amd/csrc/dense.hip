@@ -3,14 +3,15 @@
 // Replaces the reference's fused TPU kernel sa3jax/dense_attention.py:43-153 and the XLA chain
 // sa3jax/dit.py:185-200. Two kernels run back to back on the caller's stream:
 //
-//   dense_prep    one pass over qkv: per-head RMSNorm (dit.py:45-57) and rotate-half RoPE (dit.py:90-98) of
-//                 q, k, q_diff, k_diff, V * mask (dit.py:174-175), written in bf16 to a workspace. q and
-//                 q_diff also carry the softmax scale (SoftmaxPlan). V stays row-major; the attention kernel
-//                 reads its MFMA operand with gfx950's transposing LDS loads.
-//   dense_attend  flash-style single pass per (batch, head, 128-query block): K, K_diff and V tiles of 64 keys
-//                 are double-buffered through LDS; S^T = K Q^T and O^T += V^T P^T on
-//                 v_mfma_f32_32x32x16_bf16 with fp32 accumulation; both branches share each V tile; scores
-//                 never leave registers; the subtraction is done in fp32 with one cast (dense_attention.py:94).
+//   dense_prep    one pass over the key side of qkv: per-head RMSNorm (dit.py:45-57) and rotate-half RoPE
+//                 (dit.py:90-98) of k and k_diff, and V * mask (dit.py:174-175), written in bf16 to a workspace;
+//                 V is stored transposed per 64-key tile, in the order the PV MFMA consumes it.
+//   dense_attend  flash-style single pass per (batch, head, 128-query block). Each wave first prepares its own
+//                 query rows straight from qkv (RMSNorm, RoPE and the softmax scale, the same cast points), so
+//                 q and q_diff never round-trip through HBM. K, K_diff and V tiles of 64 keys are then
+//                 double-buffered through LDS; S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x16_bf16 with
+//                 fp32 accumulation; both branches share each V tile; scores never leave registers; the
+//                 subtraction is done in fp32 with one cast (dense_attention.py:94).
 //
 // Softmax without a running max. The logits are bounded a priori: after RMSNorm every row has
 // |x| <= sqrt(D) * max|w|, and RoPE is a rotation, so |s| <= D * max|w_q| * max|w_k| * log2(e)/sqrt(D). When
@@ -64,14 +65,13 @@ __device__ __forceinline__ SoftmaxPlan dense_plan(const float* __restrict__ qw, 
   return softmax_plan(rd * wave_max(mq), rd * wave_max(mk), D);
 }
 
-// RMSNorm + RoPE of q, k, q_diff, k_diff and V * mask for 64 tokens of one head. Thread task = (token, RoPE
-// group pair): the thread loads the pair's 16 dims of all four q/k sections and the pair's cos/sin slice once,
-// so every load is issued before any arithmetic; the RMS statistic is reduced over the D/16 lanes of a token.
-// RoPE reads the (L, half) fp32 tables; `half` is a multiple of 8 (checked on the host).
+// RMSNorm + RoPE of k and k_diff and V * mask for 64 tokens of one head. Thread task = (token, RoPE group pair):
+// the thread loads the pair's 16 dims of both key sections and the pair's cos/sin slice once, so every load is
+// issued before any arithmetic; the RMS statistic is reduced over the D/16 lanes of a token. RoPE reads the
+// (L, half) fp32 tables; `half` is a multiple of 8 (checked on the host). Workspace regions: k', k_diff', V'^T.
 template <int D>
 __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restrict__ qkv, int64_t rs,
-                                                       const float* __restrict__ qw, const float* __restrict__ kw,
-                                                       const float* __restrict__ cosT,
+                                                       const float* __restrict__ kw, const float* __restrict__ cosT,
                                                        const float* __restrict__ sinT, int half,
                                                        const float* __restrict__ vmask, int L, int Lp, int H,
                                                        float eps, int64_t region, uint16_t* __restrict__ ws) {
@@ -84,10 +84,9 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
   const int64_t bh = static_cast<int64_t>(b) * H + h;
   const int64_t HD = static_cast<int64_t>(H) * D;
   const int h8 = half / 8;
-  const float qscale = dense_plan<D>(qw, kw).qscale;
 
-  // Issue every global load first: 4 sections x 2 groups of data, the cos/sin slice and the V chunks.
-  u32x4 raw[TASKS][4][2];
+  // Issue every global load first: 2 sections x 2 groups of data, the cos/sin slice and the V chunks.
+  u32x4 raw[TASKS][2][2];
   f32x4 cs[TASKS][4];
   int tm1[TASKS], tm2[TASKS];
   bool trot[TASKS];
@@ -98,8 +97,8 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     trot[i] = p < h8;
     const uint16_t* row = qkv + (static_cast<int64_t>(b) * L + (l < L ? l : 0)) * rs + h * D;
 #pragma unroll
-    for (int si = 0; si < 4; ++si) {
-      const int sec = si < 2 ? si : si + 1;  // q, k, q_diff, k_diff
+    for (int si = 0; si < 2; ++si) {
+      const int sec = 1 + 3 * si;  // k, k_diff
       raw[i][si][0] = l < L ? ld16(row + sec * HD + 8 * tm1[i]) : u32x4{0u, 0u, 0u, 0u};
       raw[i][si][1] = l < L ? ld16(row + sec * HD + 8 * tm2[i]) : u32x4{0u, 0u, 0u, 0u};
     }
@@ -127,9 +126,7 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     const int task = t + 256 * i, l = l0 + task / PAIRS;
     const int m1 = tm1[i], m2 = tm2[i];
 #pragma unroll
-    for (int si = 0; si < 4; ++si) {
-      const bool isq = (si & 1) == 0;
-      const float* w = isq ? qw : kw;
+    for (int si = 0; si < 2; ++si) {
       float x1[8], x2[8];
       unpack8(raw[i][si][0], x1);
       unpack8(raw[i][si][1], x2);
@@ -142,8 +139,8 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
       float y1[8], y2[8], o1[8], o2[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {  // RMSNorm (dit.py:56-57): x * rsqrt(mean + eps), * w, cast
-        y1[j] = round_bf16((x1[j] * inv) * w[8 * m1 + j]);
-        y2[j] = round_bf16((x2[j] * inv) * w[8 * m2 + j]);
+        y1[j] = round_bf16((x1[j] * inv) * kw[8 * m1 + j]);
+        y2[j] = round_bf16((x2[j] * inv) * kw[8 * m2 + j]);
       }
       if (trot[i]) {
         const float c[8] = {cs[i][0][0], cs[i][0][1], cs[i][0][2], cs[i][0][3],
@@ -160,13 +157,6 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
         for (int j = 0; j < 8; ++j) {
           o1[j] = y1[j];
           o2[j] = y2[j];
-        }
-      }
-      if (isq) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          o1[j] = round_bf16(o1[j] * qscale);
-          o2[j] = round_bf16(o2[j] * qscale);
         }
       }
       if (l >= L) {
@@ -204,7 +194,7 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     u32x4 w;
 #pragma unroll
     for (int j = 0; j < 4; ++j) w[j] = static_cast<uint32_t>(e[2 * j]) | (static_cast<uint32_t>(e[2 * j + 1]) << 16);
-    st16(ws + 4 * region + (bh * Lp + l0) * D + d * 64 + pos0, w);
+    st16(ws + 2 * region + (bh * Lp + l0) * D + d * 64 + pos0, w);
   }
 }
 
@@ -225,9 +215,44 @@ struct DenseTile {
   static constexpr int NBLK = 3 * BPT;            // blocks per tile (a multiple of the 4 waves)
 };
 
+// Copies 64-key tile t of K, K_diff and V'^T from the workspace straight into an LDS stage (global_load_lds, no
+// registers). Each wave copies 1 KB blocks: lane i lands at byte 16 i of its block, so it fetches the chunk that
+// the swizzled layout puts there.
+template <int D>
+struct TileCopy {
+  const uint16_t* Kb;
+  const uint16_t* Kdb;
+  const uint16_t* Vb;
+  int wv;
+  uint32_t off64, off128;  // byte offset of this lane's chunk inside its wave's 1 KB block, per row length
+
+  __device__ TileCopy(const uint16_t* k, const uint16_t* kd, const uint16_t* v) : Kb(k), Kdb(kd), Vb(v) {
+    const int tid = threadIdx.x, ln = tid & 63;
+    wv = tid >> 6;
+    // The same for every block of a tensor, since the swizzle depends on the row only through bits the block
+    // index does not change.
+    const int r64 = ln >> 3;   // rows of 64 elements: 8 per block
+    off64 = static_cast<uint32_t>(wv * 1024 + r64 * 128 + 16 * ((ln & 7) ^ (r64 & 7) ^ (wv & 1)));
+    const int r128 = ln >> 4;  // rows of 128 elements: 4 per block
+    off128 = static_cast<uint32_t>(wv * 1024 + r128 * 256 + 16 * ((ln & 15) ^ (4 * (wv & 3) + r128)));
+  }
+
+  __device__ __forceinline__ void operator()(int t, uint16_t* s) const {
+    using T = DenseTile<D>;
+#pragma unroll
+    for (int tsr = 0; tsr < 3; ++tsr) {  // K, K_diff [key][d]; V^T [d][pos]
+      const uint16_t* base = (tsr == 0 ? Kb : tsr == 1 ? Kdb : Vb) + static_cast<int64_t>(t) * 64 * D;
+      const uint32_t off = tsr < 2 && D == 128 ? off128 : off64;
+#pragma unroll
+      for (int u = 0; u < T::BPT / 4; ++u)  // blocks wv, wv + 4, ...
+        lds_dma16(base, off + u * 4096, s + tsr * T::K_ELEMS + (wv + 4 * u) * 512);
+    }
+  }
+};
+
+// The key loop. Tile 0 has already been issued into stage A by the caller.
 template <int D, bool FAST>
-__device__ __forceinline__ void dense_attend_loop(const uint16_t* __restrict__ Kb, const uint16_t* __restrict__ Kdb,
-                                                  const uint16_t* __restrict__ Vb, int L, int br0, uint16_t* sA,
+__device__ __forceinline__ void dense_attend_loop(const TileCopy<D>& issue, int L, int br0, uint16_t* sA,
                                                   uint16_t* sB,
                                                   const u32x4 (&qf)[DenseTile<D>::NB][DenseTile<D>::NCT][D / 16],
                                                   f32x16 (&o)[DenseTile<D>::NB][DenseTile<D>::NCT][D / 32],
@@ -242,26 +267,8 @@ __device__ __forceinline__ void dense_attend_loop(const uint16_t* __restrict__ K
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) m[br][ct] = -INFINITY;
 
-  // The next tile is copied from the workspace straight into the other LDS stage (global_load_lds, no
-  // registers) while the current one is attended; one wait and one barrier per tile. Each wave copies 1 KB
-  // blocks: lane i lands at byte 16 i of its block, so it fetches the chunk that the swizzled layout puts there.
-  const int wv = tid >> 6, ln = tid & 63;
-  // Byte offset of this lane's chunk inside its wave's 1 KB block; the same for every block of a tensor, since
-  // the swizzle depends on the row only through bits the block index does not change.
-  const int r64 = ln >> 3;                                   // rows of 64 elements: 8 per block
-  const uint32_t off64 = static_cast<uint32_t>(wv * 1024 + r64 * 128 + 16 * ((ln & 7) ^ (r64 & 7) ^ (wv & 1)));
-  const int r128 = ln >> 4;                                  // rows of 128 elements: 4 per block
-  const uint32_t off128 = static_cast<uint32_t>(wv * 1024 + r128 * 256 + 16 * ((ln & 15) ^ (4 * (wv & 3) + r128)));
-  auto issue = [&](int t, uint16_t* s) {
-#pragma unroll
-    for (int tsr = 0; tsr < 3; ++tsr) {  // K, K_diff [key][d]; V^T [d][pos]
-      const uint16_t* base = (tsr == 0 ? Kb : tsr == 1 ? Kdb : Vb) + static_cast<int64_t>(t) * 64 * D;
-      const uint32_t off = tsr < 2 && D == 128 ? off128 : off64;
-#pragma unroll
-      for (int u = 0; u < T::BPT / 4; ++u)  // blocks wv, wv + 4, ...
-        lds_dma16(base, off + u * 4096, s + tsr * T::K_ELEMS + (wv + 4 * u) * 512);
-    }
-  };
+  // The next tile is copied into the other LDS stage while the current one is attended; one wait and one
+  // barrier per tile.
   const int lr = tid & 31, lh = (tid >> 5) & 1;
   auto attend = [&](const uint16_t* s, bool masked, int kt0) {
     attend_tile<D, NB, NCT, FAST>(
@@ -277,7 +284,6 @@ __device__ __forceinline__ void dense_attend_loop(const uint16_t* __restrict__ K
   // A copy has landed once this wave's vector-memory counter drains (s_waitcnt 0); the barrier then publishes
   // every wave's copies.
   const int nfull = L / 64;
-  issue(0, sA);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   int t = 0;
@@ -301,10 +307,61 @@ __device__ __forceinline__ void dense_attend_loop(const uint16_t* __restrict__ K
   if (nfull < nkt) attend((nfull & 1) ? sB : sA, true, nfull * 64);  // the ragged last tile
 }
 
+// RMSNorm (dit.py:45-57), rotate-half RoPE over the first 2 * 8 H8 dims (dit.py:90-98) and the softmax scale of
+// one query row, held whole by this lane: `row` points at its D elements in qkv, `cs` / `sn` at its (half)
+// columns of the tables. Cast points are those of the reference fused kernel: bf16 after the gain, after the
+// rotation and after the scale. The rotary width is a template parameter so that the partner of every dim is a
+// fixed register. Rows at or past L (`live` false) give zeros.
+template <int D, int H8>
+__device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, bool live, const float* __restrict__ qw,
+                                           const float* __restrict__ cs, const float* __restrict__ sn, float eps,
+                                           float qscale, u32x4 (&out)[D / 8]) {
+  u32x4 raw[D / 8];
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) raw[c] = ld16(row + 8 * c);
+  float cv[8 * H8 + 1], sv[8 * H8 + 1];
+#pragma unroll
+  for (int j4 = 0; j4 < 2 * H8; ++j4) {
+    const f32x4 c4 = *reinterpret_cast<const f32x4*>(cs + 4 * j4);
+    const f32x4 s4 = *reinterpret_cast<const f32x4*>(sn + 4 * j4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      cv[4 * j4 + e] = c4[e];
+      sv[4 * j4 + e] = s4[e];
+    }
+  }
+  float y[D];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    unpack8(raw[c], *reinterpret_cast<float(*)[8]>(y + 8 * c));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = __fmaf_rn(y[8 * c + j], y[8 * c + j], ss);
+  }
+  const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int d = 0; d < D; ++d) y[d] = round_bf16((y[d] * inv) * qw[d]);
+#pragma unroll
+  for (int d = 0; d < 8 * H8; ++d) {  // d < half takes -x[d + half], d >= half takes x[d - half]
+    const float y1 = y[d], y2 = y[d + 8 * H8];
+    y[d] = round_bf16(y1 * cv[d] + (-y2) * sv[d]);
+    y[d + 8 * H8] = round_bf16(y2 * cv[d] + y1 * sv[d]);
+  }
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = live ? round_bf16(y[8 * c + j] * qscale) : 0.f;
+    out[c] = pack8(o);
+  }
+}
+
 template <int D>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
-    const uint16_t* __restrict__ ws, int64_t region, int B, int L, int Lp, int H, const float* __restrict__ qw,
-    const float* __restrict__ kw, const float* __restrict__ lam, uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ qkv, int64_t rs, const float* __restrict__ cosT, const float* __restrict__ sinT,
+    int half, float eps, const uint16_t* __restrict__ ws, int64_t region, int B, int L, int Lp, int H,
+    const float* __restrict__ qw, const float* __restrict__ kw, const float* __restrict__ lam,
+    uint16_t* __restrict__ out) {
   using T = DenseTile<D>;
   constexpr int NB = T::NB, NCT = T::NCT;
   // Stages A and B of the K/V tiles; the epilogue reuses the first 32 KB as its exchange buffer.
@@ -320,14 +377,53 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
   // Launch-uniform choice between the max-free and the running-max softmax (see the file comment).
   const SoftmaxPlan plan = dense_plan<D>(qw, kw);
 
+  // The queries: each lane prepares one whole row from qkv (D = 64: row q0 + lane of this wave's branch; D = 128:
+  // row q0 + lane % 32 of branch lane / 32), then v_permlane32_swap moves the 16-byte chunks into the MFMA B
+  // operand layout (lane (lr, lh) holds chunks 2 kk + lh of its row): for chunk pair (2 kk, 2 kk + 1) the swap
+  // gives [lanes 0-31 of chunk 2 kk | lanes 0-31 of chunk 2 kk + 1] and the same for lanes 32-63.
   u32x4 qf[NB][NCT][D / 16];
+  {
+    const int64_t HD = static_cast<int64_t>(H) * D;
+    const int qrow = T::SPLIT ? q0 + lane : q0 + lr;
+    const int sec = 3 * (T::SPLIT ? br0 : lh);  // q is section 0 of a qkv row, q_diff section 3
+    const bool live = qrow < L;
+    const int qc = live ? qrow : L - 1;
+    const uint16_t* row = qkv + (static_cast<int64_t>(b) * L + qc) * rs + sec * HD + h * D;
+    const float* cs = cosT + static_cast<int64_t>(qc) * half;
+    const float* sn = sinT + static_cast<int64_t>(qc) * half;
+    u32x4 whole[D / 8];
+    switch (half / 8) {  // half % 8 == 0 and half <= D / 2 are checked on the host
+      case 0: prep_q_row<D, 0>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 1: prep_q_row<D, 1>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 2: prep_q_row<D, 2>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 3: prep_q_row<D, 3>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+      default:
+        if constexpr (D == 64) {
+          prep_q_row<D, 4>(row, live, qw, cs, sn, eps, plan.qscale, whole);
+        } else {
+          switch (half / 8) {
+            case 4: prep_q_row<D, 4>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 5: prep_q_row<D, 5>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 6: prep_q_row<D, 6>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 7: prep_q_row<D, 7>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+            default: prep_q_row<D, 8>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+          }
+        }
+    }
 #pragma unroll
-  for (int bi = 0; bi < NB; ++bi)
+    for (int kk = 0; kk < D / 16; ++kk)
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk)  // q' is region 0, q_diff' region 2
-        qf[bi][ct][kk] = ld16(ws + (br0 + bi) * 2 * region + (rowbase + q0 + 32 * ct + lr) * D + 16 * kk + 8 * lh);
+      for (int e = 0; e < 4; ++e) {
+        const auto r = __builtin_amdgcn_permlane32_swap(whole[2 * kk][e], whole[2 * kk + 1][e], false, false);
+        if constexpr (T::SPLIT) {  // lanes 0-31 held rows q0 .. q0 + 31 (column tile 0), lanes 32-63 the next 32
+          qf[0][0][kk][e] = r[0];
+          qf[0][1][kk][e] = r[1];
+        } else {  // lanes 0-31 held branch 1, lanes 32-63 branch 2, both for rows q0 .. q0 + 31
+          qf[0][0][kk][e] = r[0];
+          qf[1][0][kk][e] = r[1];
+        }
+      }
+  }
 
   f32x16 o[NB][NCT][D / 32];
   float lsum[NB][NCT];
@@ -340,13 +436,12 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
       for (int dt = 0; dt < D / 32; ++dt) o[bi][ct][dt] = f32x16{};
     }
 
-  const uint16_t* Kb = ws + region + rowbase * D;
-  const uint16_t* Kdb = ws + 3 * region + rowbase * D;
-  const uint16_t* Vb = ws + 4 * region + rowbase * D;
+  const TileCopy<D> copy(ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D);
+  copy(0, smem);
   if (plan.fast)
-    dense_attend_loop<D, true>(Kb, Kdb, Vb, L, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
+    dense_attend_loop<D, true>(copy, L, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
   else
-    dense_attend_loop<D, false>(Kb, Kdb, Vb, L, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
+    dense_attend_loop<D, false>(copy, L, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
 
   const float lamh = lam ? lam[h] : 1.f;
   if constexpr (T::SPLIT) {
@@ -445,61 +540,73 @@ extern "C" int hb_rope_tables(hipStream_t stream, const float* inv_freq, int hal
   return launch_status("rope_tables");
 }
 
-extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride, const float* q_weight,
-                             const float* k_weight, const float* cos, const float* sin, int half, const float* vmask,
-                             int B, int L, int H, int D, float eps, void* workspace, size_t workspace_bytes) {
+// Checks shared by both stages: shapes, pointers, alignment and the workspace size.
+static int dense_checks(const void* qkv, int dtype, int64_t row_stride, const float* qw, const float* kw,
+                        const float* cos, const float* sin, int half, int B, int L, int H, int D, float eps,
+                        const void* workspace, size_t workspace_bytes, DenseLayout& lay) {
   int st = hb_dense_validate(dtype, row_stride, B, L, H, D, half, eps);
   if (st) return st;
-  const DenseLayout lay = dense_layout(dtype, B, L, H, D);
-  st = dense_args(qkv, q_weight, k_weight, cos, sin, half, workspace, workspace_bytes, lay.total_bytes);
+  lay = dense_layout(dtype, B, L, H, D);
+  st = dense_args(qkv, qw, kw, cos, sin, half, workspace, workspace_bytes, lay.total_bytes);
   if (st) return st;
   if (half % 8 != 0) return fail(HB_ERR_HALF, "dense kernel needs half %% 8 == 0 (half=%d)", half);
   if (half > 0 && (reinterpret_cast<uintptr_t>(cos) % 16 || reinterpret_cast<uintptr_t>(sin) % 16))
     return fail(HB_ERR_STRIDE, "cos and sin must be 16-byte aligned");
+  return HB_OK;
+}
+
+extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride, const float* q_weight,
+                             const float* k_weight, const float* cos, const float* sin, int half, const float* vmask,
+                             int B, int L, int H, int D, float eps, void* workspace, size_t workspace_bytes) {
+  DenseLayout lay;
+  const int st = dense_checks(qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, B, L, H, D, eps, workspace,
+                              workspace_bytes, lay);
+  if (st) return st;
   if (dtype == HB_F32)
-    return launch_dense_prep_f32(stream, qkv, row_stride, q_weight, k_weight, cos, sin, half, vmask, B, L, H, D, eps,
-                                 lay, workspace);
+    return launch_dense_prep_f32(stream, qkv, row_stride, k_weight, cos, sin, half, vmask, B, L, H, D, eps, lay,
+                                 workspace);
   const dim3 grid(static_cast<unsigned>(lay.Lp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
   const uint16_t* x = static_cast<const uint16_t*>(qkv);
   uint16_t* ws = static_cast<uint16_t*>(workspace);
   const int Lp = static_cast<int>(lay.Lp);
   if (D == 64)
-    hipLaunchKernelGGL(dense_prep_bf16<64>, grid, dim3(256), 0, stream, x, row_stride, q_weight, k_weight, cos, sin,
-                       half, vmask, L, Lp, H, eps, lay.region_elems, ws);
+    hipLaunchKernelGGL(dense_prep_bf16<64>, grid, dim3(256), 0, stream, x, row_stride, k_weight, cos, sin, half, vmask,
+                       L, Lp, H, eps, lay.region_elems, ws);
   else
-    hipLaunchKernelGGL(dense_prep_bf16<128>, grid, dim3(256), 0, stream, x, row_stride, q_weight, k_weight, cos, sin,
-                       half, vmask, L, Lp, H, eps, lay.region_elems, ws);
+    hipLaunchKernelGGL(dense_prep_bf16<128>, grid, dim3(256), 0, stream, x, row_stride, k_weight, cos, sin, half, vmask,
+                       L, Lp, H, eps, lay.region_elems, ws);
   return launch_status("dense_prep");
 }
 
-extern "C" int hb_dense_attend(hipStream_t stream, const void* workspace, size_t workspace_bytes, int dtype,
-                               const float* q_weight, const float* k_weight, const float* lam, void* out, int B, int L,
-                               int H, int D) {
-  int st = hb_dense_validate(dtype, static_cast<int64_t>(5) * H * D, B, L, H, D, 0, 0.f);
+extern "C" int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
+                               const float* q_weight, const float* k_weight, const float* cos, const float* sin,
+                               int half, const float* lam, void* out, int B, int L, int H, int D, float eps,
+                               const void* workspace, size_t workspace_bytes) {
+  if (!out) {
+    clear_error();
+    return fail(HB_ERR_NULL, "out must be non-NULL");
+  }
+  DenseLayout lay;
+  const int st = dense_checks(qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, B, L, H, D, eps, workspace,
+                              workspace_bytes, lay);
   if (st) return st;
-  const DenseLayout lay = dense_layout(dtype, B, L, H, D);
-  if (!workspace || !out || !q_weight || !k_weight)
-    return fail(HB_ERR_NULL, "workspace, out, q_weight and k_weight must be non-NULL");
-  if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(HB_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  if (workspace_bytes < lay.total_bytes)
-    return fail(HB_ERR_WORKSPACE, "workspace holds %zu bytes, needs %zu", workspace_bytes, lay.total_bytes);
   if (dtype == HB_F32) {
     if (reinterpret_cast<uintptr_t>(out) % 16) return fail(HB_ERR_STRIDE, "fp32 out must be 16-byte aligned");
-    return launch_dense_attend_f32(stream, workspace, lam, out, B, L, H, D, lay);
+    return launch_dense_attend_f32(stream, qkv, row_stride, q_weight, cos, sin, half, eps, workspace, lam, out, B, L, H,
+                                   D, lay);
   }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
   const int nblocks = B * H * static_cast<int>(lay.Lp / 128);
+  const uint16_t* x = static_cast<const uint16_t*>(qkv);
   const uint16_t* ws = static_cast<const uint16_t*>(workspace);
   uint16_t* o = static_cast<uint16_t*>(out);
   const int Lp = static_cast<int>(lay.Lp);
   if (D == 64)
-    hipLaunchKernelGGL(dense_attend_bf16<64>, dim3(nblocks), dim3(DenseTile<64>::NT), 0, stream, ws, lay.region_elems,
-                       B, L, Lp, H,
-                       q_weight, k_weight, lam, o);
+    hipLaunchKernelGGL(dense_attend_bf16<64>, dim3(nblocks), dim3(DenseTile<64>::NT), 0, stream, x, row_stride, cos,
+                       sin, half, eps, ws, lay.region_elems, B, L, Lp, H, q_weight, k_weight, lam, o);
   else
-    hipLaunchKernelGGL(dense_attend_bf16<128>, dim3(nblocks), dim3(DenseTile<128>::NT), 0, stream, ws,
-                       lay.region_elems, B, L, Lp, H,
-                       q_weight, k_weight, lam, o);
+    hipLaunchKernelGGL(dense_attend_bf16<128>, dim3(nblocks), dim3(DenseTile<128>::NT), 0, stream, x, row_stride, cos,
+                       sin, half, eps, ws, lay.region_elems, B, L, Lp, H, q_weight, k_weight, lam, o);
   return launch_status("dense_attend");
 }
 
@@ -514,5 +621,6 @@ extern "C" int hb_dense_diffattn(hipStream_t stream, const void* qkv, int dtype,
   int st = hb_dense_prep(stream, qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, vmask, B, L, H, D, eps,
                          workspace, workspace_bytes);
   if (st) return st;
-  return hb_dense_attend(stream, workspace, workspace_bytes, dtype, q_weight, k_weight, lam, out, B, L, H, D);
+  return hb_dense_attend(stream, qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, lam, out, B, L, H, D, eps,
+                         workspace, workspace_bytes);
 }

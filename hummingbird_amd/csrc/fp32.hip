@@ -121,13 +121,13 @@ __device__ __forceinline__ void store_diff_f32(float* __restrict__ smem, const f
   }
 }
 
-// RMSNorm (dit.py:45-57) and rotate-half RoPE (dit.py:90-98) of q, k, q_diff, k_diff and V * mask for 64 tokens
-// of one head, all in fp32, into the workspace regions q', k', q_diff', k_diff', v'. Thread task = (token, RoPE
-// group pair) as in the bf16 prep: the rotation partner of every dim is in the thread's own registers.
+// RMSNorm (dit.py:45-57) and rotate-half RoPE (dit.py:90-98) of k and k_diff and V * mask for 64 tokens of one
+// head, all in fp32, into the workspace regions k', k_diff', v'. Thread task = (token, RoPE group pair) as in the
+// bf16 prep: the rotation partner of every dim is in the thread's own registers.
 template <int D>
 __global__ __launch_bounds__(256) void dense_prep_f32(const float* __restrict__ qkv, int64_t rs,
-                                                      const float* __restrict__ qw, const float* __restrict__ kw,
-                                                      const float* __restrict__ cosT, const float* __restrict__ sinT,
+                                                      const float* __restrict__ kw, const float* __restrict__ cosT,
+                                                      const float* __restrict__ sinT,
                                                       int half, const float* __restrict__ vmask, int L, int Lp, int H,
                                                       float eps, int64_t region, float* __restrict__ ws) {
   constexpr int PAIRS = D / 16;
@@ -156,9 +156,9 @@ __global__ __launch_bounds__(256) void dense_prep_f32(const float* __restrict__ 
       }
     }
 #pragma unroll
-    for (int si = 0; si < 4; ++si) {
-      const int sec = si < 2 ? si : si + 1;  // q, k, q_diff, k_diff
-      const float* w = (si & 1) ? kw : qw;
+    for (int si = 0; si < 2; ++si) {
+      const int sec = 1 + 3 * si;  // k, k_diff
+      const float* w = kw;
       float x1[8] = {}, x2[8] = {};
       if (in) {
 #pragma unroll
@@ -202,12 +202,15 @@ __global__ __launch_bounds__(256) void dense_prep_f32(const float* __restrict__ 
       v = ld4(qkv + (static_cast<int64_t>(b) * L + l) * rs + 2 * HD + h * D + col);
       v *= vmask ? vmask[static_cast<int64_t>(b) * L + l] : 1.f;
     }
-    st4(ws + 4 * region + (bh * Lp + l) * D + col, v);
+    st4(ws + 2 * region + (bh * Lp + l) * D + col, v);
   }
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict__ ws, int64_t region, int B, int L,
+__global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict__ qkv, int64_t rs,
+                                                        const float* __restrict__ qw, const float* __restrict__ cosT,
+                                                        const float* __restrict__ sinT, int half, float eps,
+                                                        const float* __restrict__ ws, int64_t region, int B, int L,
                                                         int Lp, int H, const float* __restrict__ lam,
                                                         float* __restrict__ out) {
   using T = F32Tile<D>;
@@ -219,13 +222,44 @@ __global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict_
   const int br = wave >> 1, q0 = qb * 64 + (wave & 1) * 32;
   const int64_t rowbase = static_cast<int64_t>(bh) * Lp;
 
+  // RMSNorm (dit.py:45-57) and rotate-half RoPE (dit.py:90-98) of this lane's half row (dims lh D/2 ..) of q
+  // (branch 1, section 0) or q_diff (branch 2, section 3), from qkv; the RoPE partner (d +- half) of each group of
+  // 4 dims is loaded directly. Rows at or past L give zeros.
   float qreg[D / 2];
-  const float* qrow = ws + br * 2 * region + (rowbase + q0 + lr) * D + lh * (D / 2);  // q' region 0, q_diff' 2
+  {
+    const int q = q0 + lr, qc = q < L ? q : L - 1, h4 = half / 4;
+    const float* row = qkv + (static_cast<int64_t>(b) * L + qc) * rs + static_cast<int64_t>(3 * br) * H * D + h * D;
+    float xp[D / 2];
+    float ss = 0.f;
 #pragma unroll
-  for (int j4 = 0; j4 < D / 8; ++j4) {
-    const f32x4 v = ld4(qrow + 4 * j4);
+    for (int j4 = 0; j4 < D / 8; ++j4) {
+      const int g = lh * (D / 8) + j4;
+      const int pg = g < h4 ? g + h4 : g < 2 * h4 ? g - h4 : g;
+      const f32x4 v = ld4(row + 4 * g), p = ld4(row + 4 * pg);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) qreg[4 * j4 + e] = v[e];
+      for (int e = 0; e < 4; ++e) {
+        qreg[4 * j4 + e] = v[e];
+        xp[4 * j4 + e] = p[e];
+        ss = __fmaf_rn(v[e], v[e], ss);
+      }
+    }
+    ss += __shfl_xor(ss, 32, kWave);
+    const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int j = 0; j < D / 2; ++j) {
+      const int d = lh * (D / 2) + j;
+      const bool first = d < half, rot = d < 2 * half;
+      const int pd = first ? d + half : rot ? d - half : d;
+      const float y = __fmul_rn(__fmul_rn(qreg[j], inv), qw[d]);
+      const float yp = __fmul_rn(__fmul_rn(xp[j], inv), qw[pd]);
+      float r = y;
+      if (rot) {  // d < half takes -x[d + half], d >= half takes x[d - half]
+        const int64_t t = static_cast<int64_t>(qc) * half + (first ? d : d - half);
+        r = first ? __fadd_rn(__fmul_rn(y, cosT[t]), __fmul_rn(-yp, sinT[t]))
+                  : __fadd_rn(__fmul_rn(y, cosT[t]), __fmul_rn(yp, sinT[t]));
+      }
+      qreg[j] = q < L ? r : 0.f;
+    }
   }
   f32x16 o[D / 32];
 #pragma unroll
@@ -233,7 +267,7 @@ __global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict_
   float lsum = 0.f, m = -INFINITY;
   const float c = kLog2e / sqrtf(static_cast<float>(D));
 
-  const float* src[3] = {ws + region + rowbase * D, ws + 3 * region + rowbase * D, ws + 4 * region + rowbase * D};
+  const float* src[3] = {ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D};
   const int nkt = (L + 63) / 64;
   for (int t = 0; t < nkt; ++t) {
     // 3 tensors x 64 rows x D floats; rows past L are the zero padding of the workspace (t * 64 + 63 < Lp)
@@ -371,34 +405,36 @@ static int launched(const char* what) {
   return HB_OK;
 }
 
-int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qw, const float* kw,
-                          const float* cosT, const float* sinT, int half, const float* vmask, int B, int L, int H,
-                          int D, float eps, const DenseLayout& lay, void* ws) {
+int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* kw, const float* cosT,
+                          const float* sinT, int half, const float* vmask, int B, int L, int H, int D, float eps,
+                          const DenseLayout& lay, void* ws) {
   const dim3 grid(static_cast<unsigned>(lay.Lp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
   const float* x = static_cast<const float*>(qkv);
   float* w = static_cast<float*>(ws);
   const int Lp = static_cast<int>(lay.Lp);
   if (D == 64)
-    hipLaunchKernelGGL(dense_prep_f32<64>, grid, dim3(256), 0, stream, x, rs, qw, kw, cosT, sinT, half, vmask, L, Lp,
-                       H, eps, lay.region_elems, w);
+    hipLaunchKernelGGL(dense_prep_f32<64>, grid, dim3(256), 0, stream, x, rs, kw, cosT, sinT, half, vmask, L, Lp, H,
+                       eps, lay.region_elems, w);
   else
-    hipLaunchKernelGGL(dense_prep_f32<128>, grid, dim3(256), 0, stream, x, rs, qw, kw, cosT, sinT, half, vmask, L, Lp,
-                       H, eps, lay.region_elems, w);
+    hipLaunchKernelGGL(dense_prep_f32<128>, grid, dim3(256), 0, stream, x, rs, kw, cosT, sinT, half, vmask, L, Lp, H,
+                       eps, lay.region_elems, w);
   return launched("dense_prep_f32");
 }
 
-int launch_dense_attend_f32(hipStream_t stream, const void* ws, const float* lam, void* out, int B, int L, int H,
-                            int D, const DenseLayout& lay) {
+int launch_dense_attend_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qw, const float* cosT,
+                            const float* sinT, int half, float eps, const void* ws, const float* lam, void* out, int B,
+                            int L, int H, int D, const DenseLayout& lay) {
   const int nblocks = B * H * static_cast<int>(lay.Lp / 64);
+  const float* x = static_cast<const float*>(qkv);
   const float* w = static_cast<const float*>(ws);
   float* o = static_cast<float*>(out);
   const int Lp = static_cast<int>(lay.Lp);
   if (D == 64)
-    hipLaunchKernelGGL(dense_attend_f32<64>, dim3(nblocks), dim3(256), 0, stream, w, lay.region_elems, B, L, Lp, H,
-                       lam, o);
+    hipLaunchKernelGGL(dense_attend_f32<64>, dim3(nblocks), dim3(256), 0, stream, x, rs, qw, cosT, sinT, half, eps, w,
+                       lay.region_elems, B, L, Lp, H, lam, o);
   else
-    hipLaunchKernelGGL(dense_attend_f32<128>, dim3(nblocks), dim3(256), 0, stream, w, lay.region_elems, B, L, Lp, H,
-                       lam, o);
+    hipLaunchKernelGGL(dense_attend_f32<128>, dim3(nblocks), dim3(256), 0, stream, x, rs, qw, cosT, sinT, half, eps, w,
+                       lay.region_elems, B, L, Lp, H, lam, o);
   return launched("dense_attend_f32");
 }
 

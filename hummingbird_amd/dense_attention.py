@@ -71,7 +71,7 @@ def tables(length: int, inv_freq: torch.Tensor, valid: torch.Tensor, head_dim: i
 
 
 def workspace_bytes(dtype: torch.dtype, batch: int, length: int, num_heads: int, head_dim: int) -> int:
-    """Bytes of scratch `dense_attention` needs (prepared q/k/v in the kernel-native layout)."""
+    """Bytes of scratch `dense_attention` needs (prepared k, k_diff and v in the kernel-native layout)."""
     return int(_lib.load().hb_dense_workspace_size(dtype_code(dtype), batch, length, num_heads, head_dim))
 
 

@@ -79,7 +79,7 @@ int hb_rope_tables(hipStream_t stream, const float* inv_freq, int half, int leng
  *   dtype              : HB_BF16 or HB_F32 (of qkv and out)
  *   D                  : 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  eps >= 0
  *   workspace          : >= hb_dense_workspace_size(dtype, B, L, H, D) bytes, 256-byte aligned; holds the
- *                        prepared q/k/v for the duration of the call (stream-ordered).
+ *                        prepared k, k_diff and v for the duration of the call (stream-ordered).
  * Internally two kernels run on `stream`: hb_dense_prep then hb_dense_attend (exported separately below). */
 size_t hb_dense_workspace_size(int dtype, int B, int L, int H, int D);
 int hb_dense_validate(int dtype, int64_t row_stride, int B, int L, int H, int D, int half, float eps);
@@ -87,15 +87,18 @@ int hb_dense_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t ro
                       const float* q_weight, const float* k_weight, const float* cos, const float* sin, int half,
                       const float* vmask, const float* lam, void* out, int B, int L, int H, int D, float eps,
                       void* workspace, size_t workspace_bytes);
-/* Stage 1: RMSNorm + RoPE of q, k, q_diff, k_diff and V-masking into `workspace` (kernel-native layout). */
+/* Stage 1: RMSNorm + RoPE of k and k_diff and V-masking into `workspace` (kernel-native layout). q_weight is
+ * checked but not read. */
 int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
                   const float* q_weight, const float* k_weight, const float* cos, const float* sin, int half,
                   const float* vmask, int B, int L, int H, int D, float eps, void* workspace,
                   size_t workspace_bytes);
-/* Stage 2: both softmax attentions and the subtraction from a workspace filled by hb_dense_prep. */
-int hb_dense_attend(hipStream_t stream, const void* workspace, size_t workspace_bytes, int dtype,
-                    const float* q_weight, const float* k_weight, const float* lam, void* out,
-                    int B, int L, int H, int D);
+/* Stage 2: RMSNorm + RoPE of q and q_diff (read from the same qkv), both softmax attentions and the
+ * subtraction, against a workspace that hb_dense_prep filled from this qkv. Arguments as hb_dense_diffattn. */
+int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
+                    const float* q_weight, const float* k_weight, const float* cos, const float* sin, int half,
+                    const float* lam, void* out, int B, int L, int H, int D, float eps,
+                    const void* workspace, size_t workspace_bytes);
 
 /* ---- SAME-L band differential attention -----------------------------------------------------------------
  * Replaces band_attention.band_attention (sa3jax/band_attention.py:123-180) and the XLA chain it stands in

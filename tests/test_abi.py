@@ -85,9 +85,9 @@ def test_band_validate(lib, kw, status):
 
 
 def test_workspace_size(lib):
-    # five (B, H, Lp, D) bf16 regions with L padded to the 128-query block
-    assert lib.hb_dense_workspace_size(0, 2, 2584, 24, 64) == 5 * 2 * 24 * 2688 * 64 * 2
-    assert lib.hb_dense_workspace_size(1, 1, 1, 1, 64) == 5 * 128 * 64 * 4
+    # three (B, H, Lp, D) regions (k, k_diff, v prepared) with L padded to the 128-query block
+    assert lib.hb_dense_workspace_size(0, 2, 2584, 24, 64) == 3 * 2 * 24 * 2688 * 64 * 2
+    assert lib.hb_dense_workspace_size(1, 1, 1, 1, 64) == 3 * 128 * 64 * 4
     assert lib.hb_dense_workspace_size(0, 1, 1, 1, 96) == 0
 
 
