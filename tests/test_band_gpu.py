@@ -141,6 +141,24 @@ def test_band_120s_vs_torch_chain():
     assert_bf16_parity(got[0, -tail:, h * 64:(h + 1) * 64], ref_head[-tail:], "120s head 3 tail vs oracle")
 
 
+def test_band_380s_vs_torch_chain():
+    """The 380 s clip shape (S=261760 frames, 8 heads of 64, w=128): 4090 steps per head over the ring, checked
+    against the torch restatement of the XLA chain on the GPU (inputs drawn on the device)."""
+    S, H, D, w = 261760, 8, 64, 128
+    announce(f"band bf16 380s S={S} H={H} w={w}")
+    gen = torch.Generator(device=DEV).manual_seed(381)
+    qkv = torch.randn((1, S, 5 * H * D), device=DEV, generator=gen).to(torch.bfloat16)
+    norm = lambda: {"alpha": torch.tensor(0.5, device=DEV),  # noqa: E731
+                    "gamma": 1 + 0.02 * torch.randn(D, device=DEV, generator=gen),
+                    "beta": 0.02 * torch.randn(D, device=DEV, generator=gen)}
+    qn, kn = norm(), norm()
+    lam = 0.2 + 0.6 * torch.rand(H, device=DEV, generator=gen)
+    freq = torch.from_numpy(workloads.inv_freq(32)).to(DEV)
+    got = ba.band_attention(qkv, qn, kn, freq, H, D, w, lam=lam).float().cpu().numpy()
+    ref = xla_chain.band_chain(qkv, qn, kn, freq, H, D, w, lam=lam).float().cpu().numpy()
+    assert_bf16_parity(got, ref, "380s")
+
+
 RUNS = [  # (B, S, H, window, half, gamma_mean): several 64-query steps per workgroup, runs crossing heads/batches
     (2, 9000, 3, 128, 32, 1.0), (1, 20000, 2, 64, 16, 1.0), (2, 7001, 3, 17, 32, 1.0), (1, 18000, 1, 0, 32, 1.0),
     (1, 16500, 2, 100, 8, 1.0), (1, 9000, 3, 128, 24, 1.0), (2, 8000, 2, 128, 32, 8.0),

@@ -170,6 +170,26 @@ def test_dense_120s_vs_torch_chain():
     assert_bf16_parity(got[1, :, h * 64:(h + 1) * 64], oracle(sub, "xla")[0], "120s head 5 vs oracle")
 
 
+def test_dense_380s_vs_torch_chain():
+    """The 380 s clip shape (B=2, L=8180, 24 heads of 64): long-sequence accumulation over 128 key tiles, checked
+    against the torch restatement of the XLA chain on the GPU (inputs drawn on the device)."""
+    B, L, H, D = 2, 8180, 24, 64
+    announce(f"dense bf16 380s B={B} L={L} H={H}")
+    gen = torch.Generator(device=DEV).manual_seed(380)
+    qkv = torch.randn((B, L, 5 * H * D), device=DEV, generator=gen).to(torch.bfloat16)
+    qw = 1 + 0.02 * torch.randn(D, device=DEV, generator=gen)
+    kw = 1 + 0.02 * torch.randn(D, device=DEV, generator=gen)
+    lam = 0.2 + 0.6 * torch.rand(H, device=DEV, generator=gen)
+    valid = torch.ones((B, L), device=DEV)
+    valid[0, L - 700:] = 0
+    valid[1, L - 16:] = 0
+    freq = torch.from_numpy(workloads.inv_freq(32)).to(DEV)
+    cos, sin, mask = da.tables(L, freq, valid, D, torch.bfloat16)
+    got = da.dense_attention(qkv, qw, kw, cos, sin, mask, H, D, 32, 1e-6, lam=lam).float().cpu().numpy()
+    ref = xla_chain.dense_chain(qkv, qw, kw, freq, valid, H, D, 1e-6, lam=lam).float().cpu().numpy()
+    assert_bf16_parity(got, ref, "380s")
+
+
 def test_dense_errors_are_value_errors():
     announce("dense argument errors")
     qkv = torch.zeros((1, 8, 5 * 2 * 96), device=DEV, dtype=torch.bfloat16)
