@@ -425,36 +425,36 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
         if (++i > ihi) break;
       }
 
-      // Branch 2 publishes lam * O2 / l2 (rounded per element); branch 1 subtracts it from O1 / l1.
+      // out = O1 / l1 - lam * O2 / l2, each product rounded on its own. The two branch waves of a query half
+      // split the work by output dims: branch 1 writes dims 0-31 (d-tile 0), branch 2 dims 32-63 (d-tile 1); each
+      // first publishes the product the other one needs (branch 1: O1 / l1 of d-tile 1; branch 2: lam * O2 / l2
+      // of d-tile 0).
       const float inv = __frcp_rn(lsum + __shfl_xor(lsum, 32, kWave));
-      float* xs = xbuf + qhalf * (2 * 16 * 64);
-      if (br == 1) {
-        const float li = __fmul_rn(lamh, inv);
+      const float li = br == 1 ? __fmul_rn(lamh, inv) : inv;  // this branch's factor
+      float* xs = xbuf + qhalf * (2 * 16 * 64);                // [d-tile][register][lane]
+      const int give = 1 - br;                                 // the d-tile the other wave stores
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) xs[(dt * 16 + r) * 64 + lane] = __fmul_rn(o[dt][r], li);
-      }
+      for (int r = 0; r < 16; ++r) xs[(give * 16 + r) * 64 + lane] = __fmul_rn(o[give][r], li);
       __syncthreads();
-      if (br == 0) {
-        uint16_t* orow = a.out + (static_cast<int64_t>(b) * S + q) * HD + h * D;
+      {
+        const int dt = br;  // the d-tile this wave stores
+        uint16_t* orow = a.out + (static_cast<int64_t>(b) * S + q) * HD + h * D + 32 * dt;
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
+        for (int g = 0; g < 4; ++g) {
+          float v[4];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float v[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              const int r = 4 * g + jj;
-              v[jj] = __fsub_rn(__fmul_rn(o[dt][r], inv), xs[(dt * 16 + r) * 64 + lane]);
-            }
-            if (q < S) {
-              u32x2 pk;
-              pk[0] = pack_bf16x2(v[0], v[1]);
-              pk[1] = pack_bf16x2(v[2], v[3]);
-              *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * lh) = pk;
-            }
+          for (int jj = 0; jj < 4; ++jj) {
+            const int r = 4 * g + jj;
+            const float mine = __fmul_rn(o[dt][r], li), other = xs[(dt * 16 + r) * 64 + lane];
+            v[jj] = br == 0 ? __fsub_rn(mine, other) : __fsub_rn(other, mine);
           }
+          if (q < S) {
+            u32x2 pk;
+            pk[0] = pack_bf16x2(v[0], v[1]);
+            pk[1] = pack_bf16x2(v[2], v[3]);
+            *reinterpret_cast<u32x2*>(orow + 8 * g + 4 * lh) = pk;
+          }
+        }
       }
       __syncthreads();
     }
