@@ -311,9 +311,10 @@ __device__ __forceinline__ void dense_attend_loop(const TileCopy<D>& issue, int 
 // one query row, held whole by this lane: `row` points at its D elements in qkv, `cs` / `sn` at its (half)
 // columns of the tables. Cast points are those of the reference fused kernel: bf16 after the gain, after the
 // rotation and after the scale. The rotary width is a template parameter so that the partner of every dim is a
-// fixed register. Rows at or past L (`live` false) give zeros.
+// fixed register. Rows at or past L are prepared from row L - 1 (the caller clamps `row`); their outputs are
+// never stored, and real rows keep the logits within the softmax plan's bound.
 template <int D, int H8>
-__device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, bool live, const float* __restrict__ qw,
+__device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, const float* __restrict__ qw,
                                            const float* __restrict__ cs, const float* __restrict__ sn, float eps,
                                            float qscale, u32x4 (&out)[D / 8]) {
   u32x4 raw[D / 8];
@@ -351,8 +352,8 @@ __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, boo
   for (int c = 0; c < D / 8; ++c) {
     float o[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = live ? round_bf16(y[8 * c + j] * qscale) : 0.f;
-    out[c] = pack8(o);
+    for (int j = 0; j < 8; ++j) o[j] = y[8 * c + j] * qscale;
+    out[c] = pack8(o);  // the packing conversion is the final bf16 rounding
   }
 }
 
@@ -386,27 +387,26 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
     const int64_t HD = static_cast<int64_t>(H) * D;
     const int qrow = T::SPLIT ? q0 + lane : q0 + lr;
     const int sec = 3 * (T::SPLIT ? br0 : lh);  // q is section 0 of a qkv row, q_diff section 3
-    const bool live = qrow < L;
-    const int qc = live ? qrow : L - 1;
+    const int qc = qrow < L ? qrow : L - 1;
     const uint16_t* row = qkv + (static_cast<int64_t>(b) * L + qc) * rs + sec * HD + h * D;
     const float* cs = cosT + static_cast<int64_t>(qc) * half;
     const float* sn = sinT + static_cast<int64_t>(qc) * half;
     u32x4 whole[D / 8];
     switch (half / 8) {  // half % 8 == 0 and half <= D / 2 are checked on the host
-      case 0: prep_q_row<D, 0>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 1: prep_q_row<D, 1>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 2: prep_q_row<D, 2>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 3: prep_q_row<D, 3>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 0: prep_q_row<D, 0>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 1: prep_q_row<D, 1>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 2: prep_q_row<D, 2>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 3: prep_q_row<D, 3>(row, qw, cs, sn, eps, plan.qscale, whole); break;
       default:
         if constexpr (D == 64) {
-          prep_q_row<D, 4>(row, live, qw, cs, sn, eps, plan.qscale, whole);
+          prep_q_row<D, 4>(row, qw, cs, sn, eps, plan.qscale, whole);
         } else {
           switch (half / 8) {
-            case 4: prep_q_row<D, 4>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 5: prep_q_row<D, 5>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 6: prep_q_row<D, 6>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 7: prep_q_row<D, 7>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
-            default: prep_q_row<D, 8>(row, live, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 4: prep_q_row<D, 4>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 5: prep_q_row<D, 5>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 6: prep_q_row<D, 6>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 7: prep_q_row<D, 7>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            default: prep_q_row<D, 8>(row, qw, cs, sn, eps, plan.qscale, whole); break;
           }
         }
     }
