@@ -6,8 +6,8 @@
 //   dense_prep    one pass over the key side of qkv: per-head RMSNorm (dit.py:45-57) and rotate-half RoPE
 //                 (dit.py:90-98) of k and k_diff, and V * mask (dit.py:174-175), written in bf16 to a workspace;
 //                 V is stored transposed per 64-key tile, in the order the PV MFMA consumes it.
-//   dense_attend  flash-style single pass per (batch, head, 128-query block). Each wave first prepares its own
-//                 query rows straight from qkv (RMSNorm, RoPE and the softmax scale, the same cast points), so
+//   dense_attend  flash-style single pass per (batch, head, 128-query block). Each lane first prepares one
+//                 query row straight from qkv (RMSNorm, RoPE and the softmax scale, the same cast points), so
 //                 q and q_diff never round-trip through HBM. K, K_diff and V tiles of 64 keys are then
 //                 double-buffered through LDS; S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_32x32x16_bf16 with
 //                 fp32 accumulation; both branches share each V tile; scores never leave registers; the
@@ -34,7 +34,9 @@ __device__ __forceinline__ int v_tile_key(int pos) { return (pos & ~12) | ((pos 
 // Asynchronous 16-byte copy global -> LDS for a whole wave: lane i's 16 bytes at `sbase` + `voff` bytes
 // (`sbase` wave-uniform) land at byte 16 i of the 1 KB LDS block `dst` (wave-uniform). Issued as inline assembly
 // so that the compiler does not serialise it against the LDS reads of the other stage; the caller waits for it
-// (s_waitcnt vmcnt(0)) before the barrier that publishes the stage.
+// (s_waitcnt vmcnt(0)) before the barrier that publishes the stage. The assembly writes M0 (the LDS address of
+// the copy); nothing else in these kernels reads M0, so the compiler's note that a reserved register in a
+// clobber list may not be preserved has no consumer here.
 __device__ __forceinline__ void lds_dma16(const void* sbase, uint32_t voff, uint16_t* dst) {
   const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
       (__attribute__((address_space(3))) uint16_t*)dst));
@@ -51,8 +53,8 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   else return row * RL + 8 * (chunk ^ (row & 15));
 }
 
-// After RMSNorm a row has |x| <= sqrt(D) * max|w|, so the plan depends only on the two gain vectors; the prep
-// and attention kernels evaluate it identically.
+// After RMSNorm a row has |x| <= sqrt(D) * max|w|, so the plan depends only on the two gain vectors and is the
+// same for every wave of the launch.
 template <int D>
 __device__ __forceinline__ SoftmaxPlan dense_plan(const float* __restrict__ qw, const float* __restrict__ kw) {
   const int lane = threadIdx.x & 63;
