@@ -107,3 +107,20 @@ def test_errors_map_to_python_exceptions(lib):
         _lib.check(dense_validate(lib, D=96), "dense")
     with pytest.raises(TypeError):
         _lib.check(dense_validate(lib, dtype=7), "dense")
+
+
+def test_workspace_and_alignment_errors_before_any_launch(lib):
+    """Too small or misaligned workspaces and misaligned inputs are rejected with their status codes before any
+    GPU call (fake, never dereferenced addresses; the checks read only the pointer values)."""
+    B, L, H, D = 1, 200, 2, 64
+    need = lib.hb_dense_workspace_size(0, B, L, H, D)
+    qkv, w, tab, ws = 0x10000, 0x20000, 0x30000, 0x40000  # 256-byte aligned stand-ins
+    args = lambda qkv=qkv, ws=ws, wsb=need, cos=tab: (None, qkv, 0, 5 * H * D, w, w, cos, cos, 32, None, None,  # noqa: E731
+                                                      0x50000, B, L, H, D, 1e-6, ws, wsb)
+    assert lib.hb_dense_diffattn(*args(wsb=need - 1)) == 8                  # HB_ERR_WORKSPACE: too small
+    assert "workspace" in lib.hb_last_error().decode()
+    assert lib.hb_dense_diffattn(*args(ws=ws + 16)) == 8                    # HB_ERR_WORKSPACE: not 256-aligned
+    assert lib.hb_dense_diffattn(*args(qkv=qkv + 2)) == 7                   # HB_ERR_STRIDE: qkv not 16-aligned
+    assert lib.hb_dense_diffattn(*args(cos=tab + 4)) == 7                   # HB_ERR_STRIDE: tables not 16-aligned
+    st = lib.hb_band_diffattn(None, qkv + 2, 0, 5 * H * D, w, w, tab, tab, 32, 16, None, 0x50000, B, L, H, D)
+    assert st == 7

@@ -190,6 +190,44 @@ def test_dense_380s_vs_torch_chain():
     assert_bf16_parity(got, ref, "380s")
 
 
+def test_dense_split_entry_points_match_the_fused_call():
+    """hb_dense_prep + hb_dense_attend (the two stages the fused entry point runs) give bit-identical output, and
+    repeated hb_dense_attend calls on one prepared workspace are stable (the benchmark times them that way)."""
+    from hummingbird_amd import _lib
+
+    announce("dense split entry points")
+    B, L, H, D = 2, 333, 3, 64
+    inp = workloads.dense_inputs(B, L, H, D, seed=33, half=16, ragged=True)
+    qkv = torch.from_numpy(inp["qkv"]).to(DEV, torch.bfloat16)
+    qw, kw = torch.from_numpy(inp["q_weight"]).to(DEV), torch.from_numpy(inp["k_weight"]).to(DEV)
+    lam = torch.from_numpy(inp["lam"]).to(DEV)
+    cos, sin, mask = da.tables(L, torch.from_numpy(inp["inv_freq"]).to(DEV), torch.from_numpy(inp["valid"]).to(DEV),
+                               D, torch.bfloat16)
+    lib = _lib.load()
+    wsb = int(lib.hb_dense_workspace_size(_lib.HB_BF16, B, L, H, D))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+    full = torch.empty((B, L, H * D), dtype=torch.bfloat16, device=DEV)
+    _lib.check(lib.hb_dense_diffattn(s, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, qw.data_ptr(), kw.data_ptr(),
+                                     cos.data_ptr(), sin.data_ptr(), 16, mask.data_ptr(), lam.data_ptr(),
+                                     full.data_ptr(), B, L, H, D, 1e-6, ws.data_ptr(), wsb), "diffattn")
+    ws.fill_(0xFF)  # the stages must not depend on what the workspace held
+    _lib.check(lib.hb_dense_prep(s, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, qw.data_ptr(), kw.data_ptr(),
+                                 cos.data_ptr(), sin.data_ptr(), 16, mask.data_ptr(), B, L, H, D, 1e-6, ws.data_ptr(),
+                                 wsb), "prep")
+    outs = []
+    for _ in range(3):
+        o = torch.empty_like(full)
+        _lib.check(lib.hb_dense_attend(s, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, qw.data_ptr(), kw.data_ptr(),
+                                       cos.data_ptr(), sin.data_ptr(), 16, lam.data_ptr(), o.data_ptr(), B, L, H, D,
+                                       1e-6, ws.data_ptr(), wsb), "attend")
+        outs.append(o)
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o.view(torch.int16), full.view(torch.int16))
+    assert_bf16_parity(full.float().cpu().numpy(), oracle(inp, "xla"), "split entry points vs oracle")
+
+
 def test_dense_errors_are_value_errors():
     announce("dense argument errors")
     qkv = torch.zeros((1, 8, 5 * 2 * 96), device=DEV, dtype=torch.bfloat16)
