@@ -16,6 +16,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import sys
@@ -167,8 +168,8 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
 
         def bcall():
             _lib.check(lib.hb_band_diffattn(sp, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, qd.data_ptr(), kd.data_ptr(),
-                                            cos.data_ptr(), sin.data_ptr(), half, W, 0, out.data_ptr(), B, S, H, D),
-                       "band")
+                                            cos.data_ptr(), sin.data_ptr(), half, W, 0, out.data_ptr(), B, S, H, D,
+                                            0, 0), "band")
         pc = call_percentiles(bcall, 10, stream)
         gbs = wl.band_bytes(B, S, H, D) / (pc["p50"] * 1e-6) / 1e9
         res[f"band_{name}"] = {"shape": {"B": B, "S": S, "H": H, "D": D, "w": W, "half": half}, "us_per_call": pc,
@@ -194,7 +195,8 @@ def parity(got, ref, dtype: str) -> dict:
 
 def sweep(lib, sp, stream, dev) -> None:
     """Mixed-shape sweep: per shape, p50 per-call time, roofline fraction and parity (one JSON line each).
-    Dense: B=2, H = 1536 / D, ragged value mask (0-25 % tail per row). Band: B=1, S=16384, 8 heads of 64."""
+    Dense: B=2, H = 1536 / D, ragged value mask (0-25 % tail per row). Band: B=1, S=16384, 8 heads of 64 or 4
+    of 128, half-widths 64-512."""
     import torch
 
     from hummingbird_amd import _lib
@@ -233,9 +235,9 @@ def sweep(lib, sp, stream, dev) -> None:
                                   "peak_frac_p50": round(tf / peak, 4), **parity(out.float(), ref.float(), dt)}),
                       flush=True)
                 del qkv, ws, out, ref
-    for w in (64, 128, 256):
+    for (H, D), w in itertools.product(((8, 64), (4, 128)), (64, 128, 256, 512)):
         for dt in ("bf16", "fp32"):
-            S, H, D = 16384, 8, 64
+            S = 16384
             inp = wl.band_inputs(1, S, H, D, w, seed=w, dtype=dt)
             qkv = torch.from_numpy(inp["qkv"]).to(dev, tdt[dt])
             qn = {k: torch.as_tensor(np.asarray(v)).to(dev) for k, v in inp["q_norm"].items()}
@@ -245,11 +247,13 @@ def sweep(lib, sp, stream, dev) -> None:
             qd, kd = ba.pack_dyt(qn, D, dev), ba.pack_dyt(kn, D, dev)
             code = _lib.HB_BF16 if dt == "bf16" else _lib.HB_F32
             out = torch.empty((1, S, H * D), dtype=tdt[dt], device=dev)
+            wsb = int(lib.hb_band_workspace_size(code, 1, S, H, D, inp["half"], w))
+            ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
 
             def call():
                 _lib.check(lib.hb_band_diffattn(sp, qkv.data_ptr(), code, 5 * H * D, qd.data_ptr(), kd.data_ptr(),
                                                 cos.data_ptr(), sin.data_ptr(), inp["half"], w, lam.data_ptr(),
-                                                out.data_ptr(), 1, S, H, D), "band")
+                                                out.data_ptr(), 1, S, H, D, ws.data_ptr(), wsb), "band")
             pc = call_percentiles(call, 10, stream)
             ref = xla_chain.band_chain(qkv, qn, kn, freq, H, D, w, lam=lam)
             elem = 2 if dt == "bf16" else 4
@@ -371,7 +375,7 @@ def main() -> int:
     def band_call() -> None:
         _lib.check(lib.hb_band_diffattn(sp, qkv_b.data_ptr(), _lib.HB_BF16, 5 * HB * DB, qdyt.data_ptr(),
                                         kdyt.data_ptr(), cos_b.data_ptr(), sin_b.data_ptr(), half_b, W,
-                                        lam_b.data_ptr(), out_b.data_ptr(), 1, S, HB, DB), "band")
+                                        lam_b.data_ptr(), out_b.data_ptr(), 1, S, HB, DB, 0, 0), "band")
 
     def step() -> None:
         for i in range(wl.DENSE_CALLS_PER_CLIP):

@@ -48,7 +48,8 @@ def pack_dyt(norm: dict, head_dim: int, device: torch.device) -> torch.Tensor:
 def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torch.Tensor, num_heads: int,
                    head_dim: int, window: int, *, rows: int = 1024, halo: int = 32, sub: int = 256,
                    stack: bool = True, interpret: bool = False, lam: torch.Tensor | None = None,
-                   tables: tuple[torch.Tensor, torch.Tensor] | None = None) -> torch.Tensor:
+                   tables: tuple[torch.Tensor, torch.Tensor] | None = None,
+                   workspace: torch.Tensor | None = None) -> torch.Tensor:
     """`(B, S, 5 * H * D)` projection output -> `(B, S, H * D)` differential band attention, in `qkv.dtype`.
 
     Same contract as the reference (sa3jax/band_attention.py:123-135): `q_norm`/`k_norm` are the block's DyT
@@ -56,7 +57,9 @@ def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torc
     `|k - p| <= window` inside `[0, S)`. `rows`, `halo`, `sub`, `stack` and `interpret` are the TPU kernel's
     tiling knobs and are accepted and ignored (the reference's `halo >= window` constraint does not apply: the
     HIP kernel takes any window >= 0). `lam` `(H,)` optionally weights the second branch (default 1, the
-    reference). `tables` optionally supplies `(cos, sin)` from `rope_tables(S, inv_freq)`.
+    reference). `tables` optionally supplies `(cos, sin)` from `rope_tables(S, inv_freq)`. `workspace` optionally
+    supplies the scratch that bf16 shapes outside the streaming kernel (window > 128 or head_dim 128) need:
+    `hb_band_workspace_size` bytes of uint8 on the same device; it is allocated here when absent.
     """
     del rows, halo, sub, stack, interpret
     _require_gpu(qkv, "qkv")
@@ -93,8 +96,17 @@ def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torc
         lam_p = lam.data_ptr()
     out = torch.empty((batch, length, num_heads * head_dim), dtype=qkv.dtype, device=dev)
     lib = _lib.load()
+    need = int(lib.hb_band_workspace_size(code, batch, length, num_heads, head_dim, half, int(window)))
+    ws_p, ws_bytes = 0, 0
+    if need:  # shapes outside the streaming kernel prepare their keys into scratch
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        elif workspace.numel() * workspace.element_size() < need or workspace.device != dev:
+            raise ValueError(f"workspace must hold {need} bytes on {dev}")
+        ws_p, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     stream = torch.cuda.current_stream(dev).cuda_stream
     status = lib.hb_band_diffattn(stream, qkv.data_ptr(), code, rs, qd.data_ptr(), kd.data_ptr(), cos_p, sin_p, half,
-                                  int(window), lam_p, out.data_ptr(), batch, length, num_heads, head_dim)
+                                  int(window), lam_p, out.data_ptr(), batch, length, num_heads, head_dim, ws_p,
+                                  ws_bytes)
     _lib.check(status, "band_attention")
     return out

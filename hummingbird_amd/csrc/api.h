@@ -46,6 +46,12 @@ bool band_ring_supported(int dtype, int D, int half, int window);
 int launch_band_ring(hipStream_t stream, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
                      const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                      int S, int H);
+// Tiled band kernels (band_tiled.hip): bf16, any head_dim and half-width; the workspace holds the prepared keys
+// in the dense layout (three (B, H, round_up(S, 128), D) regions: k', k_diff', v'^T).
+DenseLayout band_tiled_layout(int B, int S, int H, int D);
+int launch_band_tiled(hipStream_t stream, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
+                      const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
+                      int S, int H, int D, void* workspace);
 int launch_band_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qdyt, const float* kdyt,
                     const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                     int S, int H, int D);

@@ -51,12 +51,6 @@ constexpr int XF = 2 * 2 * 16 * 64;  // exchange floats: 2 query halves x 2 d-ti
 __device__ __forceinline__ int kofs(int r, int c) { return r * D + 8 * (c ^ (r & 7) ^ ((r >> 3) & 1)); }
 __device__ __forceinline__ int vofs(int r, int c) { return r * D + 8 * (c ^ ((r & 3) << 1)); }
 
-// DyT(x) = gamma * tanh(alpha x) + beta with tanh(y) = 1 - 2 / (1 + 2^(2 log2(e) y)):
-// y = (gamma + beta) + (-2 gamma) / (1 + 2^(a2 x)), a2 = 2 log2(e) alpha. Two transcendental instructions.
-__device__ __forceinline__ float dyt(float x, float a2, float g2, float gb) {
-  return __fmaf_rn(g2, __builtin_amdgcn_rcpf(1.f + fast_exp2(a2 * x)), gb);
-}
-
 // Raw inputs of one prep task: groups m1, m2 of tensors A and B (k and k_diff, or q and q_diff) of one row,
 // and the cos / sin slice of frequencies 8 m1 .. 8 m1 + 7 (unused when the pair is not rotated, or half = 0).
 struct Raw {
@@ -85,8 +79,8 @@ __device__ __forceinline__ void prep_task(const Raw& r, int m1, int m2, bool rot
     unpack8(tsr ? r.b2 : r.a2, x2);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float y1 = dyt(x1[j], a2, par[8 * m1 + j], par[D + 8 * m1 + j]);
-      const float y2 = dyt(x2[j], a2, par[8 * m2 + j], par[D + 8 * m2 + j]);
+      const float y1 = dyt_tanh(x1[j], a2, par[8 * m1 + j], par[D + 8 * m1 + j]);
+      const float y2 = dyt_tanh(x2[j], a2, par[8 * m2 + j], par[D + 8 * m2 + j]);
       // rotate_half: d < half takes -x[d + half], d >= half takes x[d - half]
       o1[j] = __fmaf_rn(y1, cs[j], -(y2 * sn[j])) * scale;
       o2[j] = __fmaf_rn(y2, cs[j], y1 * sn[j]) * scale;
@@ -462,16 +456,6 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
   }
 }
 
-// |DyT(x)| bound: sqrt(sum_d (|gamma_d| + |beta_d|)^2), reduced over the wave.
-__device__ __forceinline__ float dyt_bound(const float* __restrict__ dyt) {
-  const int lane = threadIdx.x & 63;
-  const float v = fabsf(dyt[1 + lane]) + fabsf(dyt[1 + D + lane]);
-  float acc = v * v;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, kWave);
-  return sqrtf(acc);
-}
-
 template <int C>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void band_ring_bf16(Args a) {
   constexpr int RING = 2 * C + 1;
@@ -487,7 +471,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     par[2 * D + t] = -2.f * kg;
     par[3 * D + t] = kg + kb;
   }
-  const SoftmaxPlan plan = softmax_plan(dyt_bound(a.q_dyt), dyt_bound(a.k_dyt), D);
+  const SoftmaxPlan plan = softmax_plan(dyt_row_bound<D>(a.q_dyt), dyt_row_bound<D>(a.k_dyt), D);
   const float qa2 = 2.f * kLog2e * a.q_dyt[0], ka2 = 2.f * kLog2e * a.k_dyt[0];
   __syncthreads();
   if (wave_id() >= 4)

@@ -95,6 +95,28 @@ __device__ __forceinline__ void pair_groups(int p, int h8, int& m1, int& m2) {
   }
 }
 
+// DyT(x) = gamma * tanh(alpha x) + beta (sa3jax/same_l.py:58-69) with tanh(y) = 1 - 2 / (1 + 2^(2 log2(e) y)):
+// (gamma + beta) + (-2 gamma) / (1 + 2^(a2 x)), a2 = 2 log2(e) alpha, g2 = -2 gamma, gb = gamma + beta. Two
+// transcendental instructions.
+__device__ __forceinline__ float dyt_tanh(float x, float a2, float g2, float gb) {
+  return __fmaf_rn(g2, __builtin_amdgcn_rcpf(1.f + fast_exp2(a2 * x)), gb);
+}
+
+// Bound on the norm of a DyT output row: |DyT(x)_d| <= |gamma_d| + |beta_d|, so |y| <= sqrt(sum_d (|gamma_d| +
+// |beta_d|)^2) for `dyt` = [alpha, gamma[D], beta[D]]; reduced over the wave (every lane gets the value).
+template <int D>
+__device__ __forceinline__ float dyt_row_bound(const float* __restrict__ dyt) {
+  const int lane = threadIdx.x & 63;
+  float acc = 0.f;
+  for (int d = lane; d < D; d += 64) {
+    const float v = fabsf(dyt[1 + d]) + fabsf(dyt[1 + D + d]);
+    acc = __fmaf_rn(v, v, acc);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+  return sqrtf(acc);
+}
+
 // Workgroup index remap that keeps consecutive logical tiles on one XCD (its own L2). Hardware dispatches
 // workgroup p to XCD p % 8; logical tile `start(x) + p / 8` is given to it, so each XCD walks a contiguous
 // range of the logical order.

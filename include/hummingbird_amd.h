@@ -109,11 +109,18 @@ int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, int64_t row_
  * half-width (`|k - q| <= window`, sa3jax/band_attention.py:110).
  *   q_dyt, k_dyt : 1 + 2*D floats each: [alpha, gamma[0..D), beta[0..D)]
  *   cos, sin     : (S, half) floats from hb_rope_tables (ignored when half == 0)
- *   dtype        : HB_BF16 or HB_F32;  D: 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  window >= 0 */
+ *   dtype        : HB_BF16 or HB_F32;  D: 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  window >= 0
+ *   workspace    : >= hb_band_workspace_size(dtype, B, S, H, D, half, window) bytes, 256-byte aligned; that size
+ *                  is 0 (and workspace may be NULL) for fp32 and for bf16 with D = 64 and window <= 128, which
+ *                  run without one. Otherwise it holds the prepared keys for the duration of the call.
+ * Kernels: bf16 with D = 64 and window <= 128 runs one streaming kernel; other bf16 shapes run a key
+ * preparation kernel and an attention kernel over the workspace; fp32 runs one kernel. */
+size_t hb_band_workspace_size(int dtype, int B, int S, int H, int D, int half, int window);
 int hb_band_validate(int dtype, int64_t row_stride, int B, int S, int H, int D, int half, int window);
 int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
                      const float* q_dyt, const float* k_dyt, const float* cos, const float* sin, int half,
-                     int window, const float* lam, void* out, int B, int S, int H, int D);
+                     int window, const float* lam, void* out, int B, int S, int H, int D, void* workspace,
+                     size_t workspace_bytes);
 
 #ifdef __cplusplus
 }

@@ -30,7 +30,8 @@ def lib():
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for required in ("hb_dense_diffattn", "hb_band_diffattn", "hb_rope_tables", "hb_dense_prep", "hb_dense_attend",
-                     "hb_dense_workspace_size", "hb_dense_validate", "hb_band_validate", "hb_last_error"):
+                     "hb_dense_workspace_size", "hb_band_workspace_size", "hb_dense_validate", "hb_band_validate",
+                     "hb_last_error"):
         assert required in names
 
 
@@ -96,7 +97,7 @@ def test_null_pointers_are_rejected_before_any_launch(lib):
     st = lib.hb_dense_diffattn(None, None, 0, 5 * 64, None, None, None, None, 0, None, None, None, 1, 8, 1, 64,
                                1e-6, None, 0)
     assert st == 1
-    st = lib.hb_band_diffattn(None, None, 0, 5 * 64, None, None, None, None, 0, 4, None, None, 1, 8, 1, 64)
+    st = lib.hb_band_diffattn(None, None, 0, 5 * 64, None, None, None, None, 0, 4, None, None, 1, 8, 1, 64, None, 0)
     assert st == 1
     assert lib.hb_rope_tables(None, None, 4, 10, None, None) == 1
     assert lib.hb_rope_tables(None, None, 0, 10, None, None) == 0  # nothing to build
@@ -122,5 +123,12 @@ def test_workspace_and_alignment_errors_before_any_launch(lib):
     assert lib.hb_dense_diffattn(*args(ws=ws + 16)) == 8                    # HB_ERR_WORKSPACE: not 256-aligned
     assert lib.hb_dense_diffattn(*args(qkv=qkv + 2)) == 7                   # HB_ERR_STRIDE: qkv not 16-aligned
     assert lib.hb_dense_diffattn(*args(cos=tab + 4)) == 7                   # HB_ERR_STRIDE: tables not 16-aligned
-    st = lib.hb_band_diffattn(None, qkv + 2, 0, 5 * H * D, w, w, tab, tab, 32, 16, None, 0x50000, B, L, H, D)
+    st = lib.hb_band_diffattn(None, qkv + 2, 0, 5 * H * D, w, w, tab, tab, 32, 16, None, 0x50000, B, L, H, D, None, 0)
     assert st == 7
+    # bf16 with a window beyond the streaming kernel needs a workspace: missing or short ones are rejected
+    need = lib.hb_band_workspace_size(0, B, L, H, D, 32, 200)
+    assert need == 3 * B * H * 256 * D * 2
+    assert lib.hb_band_workspace_size(0, B, L, H, D, 32, 128) == 0 and lib.hb_band_workspace_size(1, B, L, H, D, 32, 200) == 0
+    band = lambda ws, wsb: lib.hb_band_diffattn(None, qkv, 0, 5 * H * D, w, w, tab, tab, 32, 200, None, 0x50000,  # noqa: E731
+                                                B, L, H, D, ws, wsb)
+    assert band(None, 0) == 8 and band(ws, need - 1) == 8 and band(ws + 64, need) == 8

@@ -1,8 +1,10 @@
 """GPU parity of the band differential attention (hb_band_diffattn) against the oracle.
 
-Small shapes (including the edges of the sequence and windows of 0, 1, 17, 64 and 128) run against the NumPy
-oracle's XLA-chain profile (the contract) and the fused-kernel profile (tighter); the 120 s shape runs
-against the torch restatement of the XLA chain on the GPU and through size-independent properties.
+Small shapes (including the edges of the sequence, windows of 0, 1, 17, 64, 128 and 400, head_dim 128) run
+against the NumPy oracle's XLA-chain profile (the contract) and the fused-kernel profile (tighter); multi-block
+shapes on both kernels (the streaming ring for w <= 128 at head_dim 64, the tiled kernels otherwise) and the
+120 s and 380 s shapes run against the torch restatement of the XLA chain on the GPU and through
+size-independent properties.
 """
 from __future__ import annotations
 
@@ -165,29 +167,49 @@ RUNS = [  # (B, S, H, window, half, gamma_mean): several 64-query steps per work
 ]
 
 
-@pytest.mark.parametrize("shape", RUNS, ids=lambda s: "B%dS%dH%dw%dh%dg%g" % s)
-def test_band_multistep_runs_vs_torch_chain(shape):
-    """Shapes with more 64-query steps than CUs, so each workgroup streams a run of steps and some runs cross a
-    (batch, head) boundary; checked against the torch restatement of the XLA chain, and the first and last
-    300 positions of the last head against the oracle (the sequence edges)."""
-    b, s, h, w, half, gm = shape
-    announce(f"band bf16 multistep {shape}")
-    inp = workloads.band_inputs(b, s, h, 64, w, seed=s + h + w, half=half, gamma_mean=gm)
+def check_vs_torch_chain(b, s, h, d, w, half, gm, label):
+    """The whole output against the torch restatement of the XLA chain, and the first and last 300 positions of
+    the last head against the oracle (the sequence edges)."""
+    inp = workloads.band_inputs(b, s, h, d, w, seed=s + h + w, half=half, gamma_mean=gm)
     got = run_hip(inp)
     qkv = torch.from_numpy(inp["qkv"]).to(DEV, torch.bfloat16)
     ref = xla_chain.band_chain(qkv, norm_t(inp["q_norm"]), norm_t(inp["k_norm"]),
-                               torch.from_numpy(inp["inv_freq"]).to(DEV), h, 64, w,
+                               torch.from_numpy(inp["inv_freq"]).to(DEV), h, d, w,
                                lam=torch.from_numpy(inp["lam"]).to(DEV)).float().cpu().numpy()
     if gm == 1.0:
-        assert_bf16_parity(got, ref, f"multistep {shape}")
+        assert_bf16_parity(got, ref, label)
     else:  # logits reach ~50 here: the XLA chain keeps q/k in fp32, the fused cast points round them to bf16
-        assert stats(got, ref)["cosine"] >= 0.999, f"multistep {shape}: {stats(got, ref)}"
+        assert stats(got, ref)["cosine"] >= 0.999, f"{label}: {stats(got, ref)}"
     hh = h - 1
-    cols = np.concatenate([np.arange(sec * h * 64 + hh * 64, sec * h * 64 + hh * 64 + 64) for sec in range(5)])
+    cols = np.concatenate([np.arange(sec * h * d + hh * d, sec * h * d + hh * d + d) for sec in range(5)])
     head = dict(inp, qkv=np.ascontiguousarray(inp["qkv"][-1:, :, cols]), heads=1, lam=inp["lam"][hh:hh + 1])
     exp = oracle(head, "xla" if gm == 1.0 else "fused")[0]
     for lo, hi in ((0, 300), (s - 300, s)):
-        assert_bf16_parity(got[-1, lo:hi, hh * 64:(hh + 1) * 64], exp[lo:hi], f"multistep {shape} [{lo},{hi}) vs oracle")
+        assert_bf16_parity(got[-1, lo:hi, hh * d:(hh + 1) * d], exp[lo:hi], f"{label} [{lo},{hi}) vs oracle")
+
+
+@pytest.mark.parametrize("shape", RUNS, ids=lambda s: "B%dS%dH%dw%dh%dg%g" % s)
+def test_band_multistep_runs_vs_torch_chain(shape):
+    """Shapes with more 64-query steps than CUs, so each workgroup streams a run of steps and some runs cross a
+    (batch, head) boundary."""
+    b, s, h, w, half, gm = shape
+    announce(f"band bf16 multistep {shape}")
+    check_vs_torch_chain(b, s, h, 64, w, half, gm, f"multistep {shape}")
+
+
+TILED = [  # (B, S, H, D, window, half, gamma_mean): windows past 128 and head_dim 128 (the tiled kernels)
+    (1, 5000, 2, 64, 256, 32, 1.0), (2, 3001, 2, 64, 129, 16, 1.0), (1, 4100, 1, 64, 700, 24, 1.0),
+    (2, 3000, 2, 128, 128, 64, 1.0), (1, 4000, 2, 128, 300, 48, 1.0), (1, 3000, 2, 128, 17, 0, 1.0),
+    (1, 3000, 2, 64, 200, 32, 8.0),
+]
+
+
+@pytest.mark.parametrize("shape", TILED, ids=lambda s: "B%dS%dH%dD%dw%dh%dg%g" % s)
+def test_band_tiled_vs_torch_chain(shape):
+    """Several 128-query blocks per head whose key windows overlap, partly in-band tiles, ragged last tiles."""
+    b, s, h, d, w, half, gm = shape
+    announce(f"band bf16 tiled {shape}")
+    check_vs_torch_chain(b, s, h, d, w, half, gm, f"tiled {shape}")
 
 
 def test_band_errors_are_value_errors():
