@@ -95,14 +95,24 @@ __device__ __forceinline__ void prep_task(const Raw& r, int m1, int m2, bool rot
   }
 }
 
-// S^T of one ring tile for an attention wave: 64 keys x its 32 queries (both 32-key halves).
-__device__ __forceinline__ void qk(const uint16_t* __restrict__ sk, const int (&koff)[4], const u32x4 (&qf)[4],
-                                   f32x16 (&sc)[2]) {
+// K fragments of one ring tile for an attention wave (key row 32 rt + lr, dims 16 kk + 8 lh .. +8).
+__device__ __forceinline__ void kload(const uint16_t* __restrict__ sk, const int (&koff)[4], u32x4 (&kf)[2][4]) {
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) kf[rt][kk] = lds16(sk + rt * 32 * D + koff[kk]);
+}
+
+// S^T of one ring tile for an attention wave: 64 keys x its 32 queries, for the 32-key halves that take part
+// (act0, act1: wave-uniform; a half that does not keeps its registers and is never read).
+__device__ __forceinline__ void qk(const u32x4 (&kf)[2][4], const u32x4 (&qf)[4], f32x16 (&sc)[2], bool act0,
+                                   bool act1) {
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
+    if (!(rt == 0 ? act0 : act1)) continue;
     sc[rt] = f32x16{};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) sc[rt] = mfma_bf16_32x32x16(lds16(sk + rt * 32 * D + koff[kk]), qf[kk], sc[rt]);
+    for (int kk = 0; kk < 4; ++kk) sc[rt] = mfma_bf16_32x32x16(kf[rt][kk], qf[kk], sc[rt]);
   }
 }
 
@@ -116,6 +126,7 @@ __device__ __forceinline__ void soft_pv(const f32x16 (&sc)[2], const uint16_t* _
                                         bool msk0, bool msk1, int lo, unsigned span) {
   const bool act[2] = {act0, act1};
   const bool msk[2] = {msk0, msk1};
+
   // A masked-out score's probability is exp2(-inf) = 0.
   auto score = [&](int rt, int r) {
     const int kc = 32 * rt + 8 * (r >> 2) + (r & 3);
@@ -393,28 +404,42 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
         const int kt = j - C + i;
         return ring + ((kt % RING + RING) % RING) * TILE;
       };
+      // 32-key half rt of tile i takes part: it meets the band of at least one query of the wave.
+      auto active = [&](int i, int rt) {
+        const int k0 = KT * (j - C + i) + 32 * rt;
+        return k0 + 31 >= ulo && k0 <= uhi;
+      };
+      auto scores = [&](int i, const u32x4 (&kf)[2][4], f32x16 (&sc)[2]) {
+        qk(kf, qf, sc, active(i, 0), active(i, 1));
+      };
+      auto frags = [&](int i, u32x4 (&kf)[2][4]) { kload(tile_ptr(i) + br * TE, koff, kf); };
       auto finish = [&](int i, const f32x16 (&sc)[2]) {
         const int kt0 = KT * (j - C + i);
         bool act[2], full[2];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
           const int k0 = kt0 + 32 * rt, k1 = k0 + 31;
-          act[rt] = k1 >= ulo && k0 <= uhi;
+          act[rt] = active(i, rt);
           full[rt] = k0 >= qa + 31 - w && k1 <= qa + w && k0 >= 0 && k1 <= S - 1;
         }
         soft_pv<FAST>(sc, tile_ptr(i) + 2 * TE, voff, o, lsum, m, c, act[0], act[1], !full[0], !full[1],
                       qlo - kt0 - 4 * lh, static_cast<unsigned>(qhi - qlo));
       };
-      // The next tile's scores are always issued (the last tile's twice), so both score buffers stay in fixed
-      // registers across the loop.
+      // The K fragments are read one tile ahead of their MFMAs. The loop is unrolled over the two score and
+      // fragment buffers so that all of them stay in fixed registers.
       f32x16 sa[2], sb[2];
-      qk(tile_ptr(ilo) + br * TE, koff, qf, sa);
+      u32x4 ka[2][4], kb[2][4];
+      frags(ilo, ka);
+      if (ilo + 1 <= ihi) frags(ilo + 1, kb);
+      scores(ilo, ka, sa);
 #pragma unroll 1
       for (int i = ilo;;) {
-        qk(tile_ptr(i + 1 <= ihi ? i + 1 : i) + br * TE, koff, qf, sb);
+        if (i + 2 <= ihi) frags(i + 2, ka);
+        if (i + 1 <= ihi) scores(i + 1, kb, sb);
         finish(i, sa);
         if (++i > ihi) break;
-        qk(tile_ptr(i + 1 <= ihi ? i + 1 : i) + br * TE, koff, qf, sa);
+        if (i + 2 <= ihi) frags(i + 2, kb);
+        if (i + 1 <= ihi) scores(i + 1, ka, sa);
         finish(i, sb);
         if (++i > ihi) break;
       }
