@@ -130,8 +130,8 @@ EXTRA_BAND = {"ref_true_120s": (1, 23086, 24, 64, 17, 16), "clip_380s": (1, 2617
 
 
 def extra_shapes(lib, sp, stream, dev) -> dict:
-    """Per-call p10/p50/p90 and roofline fractions of the dense and band calls at the extra shapes (synthetic
-    N(0,1) qkv drawn on the device, unit gains, lam = 1)."""
+    """Per-call p10/p50/p90 and roofline fractions of the dense and band calls at the extra shapes, and of the DiT
+    cross-attention at the 120 s clip (synthetic N(0,1) inputs drawn on the device, unit gains, lam = 1)."""
     import torch
 
     from hummingbird_amd import _lib
@@ -176,6 +176,32 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
                                "gbs_p50": round(gbs, 1), "hbm_frac_p50": round(gbs / HBM_PEAK_GBS, 4),
                                "tflops_p50": round(wl.band_flops(B, S, H, D, W) / (pc["p50"] * 1e-6) / 1e12, 1)}
         del qkv, out
+    # DiT cross-attention of the same clip (as many calls as the self-attention): the context's K/V prepared
+    # once, then the attention per call against it.
+    c = wl.CROSS_120S
+    B, L, Nk, H, D = c["batch"], c["length"], c["context"], c["heads"], c["head_dim"]
+    q = torch.randn((B, L, 2 * H * D), device=dev, generator=gen).to(torch.bfloat16)
+    kv = torch.randn((B, Nk, 3 * H * D), device=dev, generator=gen).to(torch.bfloat16)
+    ones = torch.ones(D, device=dev)
+    wsb = int(lib.hb_cross_workspace_size(_lib.HB_BF16, B, Nk, H, D))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    out = torch.empty((B, L, H * D), dtype=torch.bfloat16, device=dev)
+
+    def prep():
+        _lib.check(lib.hb_cross_prep(sp, kv.data_ptr(), _lib.HB_BF16, 3 * H * D, ones.data_ptr(), B, Nk, H, D, 1e-6,
+                                     ws.data_ptr(), wsb), "cross_prep")
+
+    def attend():
+        _lib.check(lib.hb_cross_attend(sp, q.data_ptr(), _lib.HB_BF16, 2 * H * D, ones.data_ptr(), ones.data_ptr(),
+                                       0, out.data_ptr(), B, L, Nk, H, D, 1e-6, ws.data_ptr(), wsb), "cross_attend")
+    pp = call_percentiles(prep, 20, stream)
+    pc = call_percentiles(attend, 20, stream)
+    tf = wl.cross_flops(B, L, Nk, H, D) / (pc["p50"] * 1e-6) / 1e12
+    res["cross_120s"] = {"shape": {"B": B, "L": L, "Nk": Nk, "H": H, "D": D}, "prep_us_per_context": pp,
+                         "us_per_call": pc, "tflops_p50": round(tf, 1),
+                         "mfma_frac_p50": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                         "ms_per_clip": round(wl.DENSE_CALLS_PER_CLIP * pc["p50"] / 1e3, 3)}
+    del q, kv, ws, out
     return res
 
 

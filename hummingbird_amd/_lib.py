@@ -39,6 +39,12 @@ SIGNATURES = {
     "hb_band_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "hb_band_diffattn": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                  c_int, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_size_t]),
+    "hb_cross_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "hb_cross_validate": (c_int, [c_int, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_float]),
+    "hb_cross_prep": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int, c_int, c_int, c_int, c_float,
+                              c_void_p, c_size_t]),
+    "hb_cross_attend": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t]),
 }
 
 _lib: ctypes.CDLL | None = None

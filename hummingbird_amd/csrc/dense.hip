@@ -44,9 +44,12 @@ __device__ __forceinline__ SoftmaxPlan dense_plan(const float* __restrict__ qw, 
 // the thread loads the pair's 16 dims of both key sections and the pair's cos/sin slice once, so every load is
 // issued before any arithmetic; the RMS statistic is reduced over the D/16 lanes of a token. RoPE reads the
 // (L, half) fp32 tables; `half` is a multiple of 8 (checked on the host). Workspace regions: k', k_diff', V'^T.
+// `sk`, `skd`, `sv`: the sections of k, k_diff and v in a row of `qkv`, in units of H * D elements (self-attention
+// reads a to_qkv row [q | k | v | q_diff | k_diff], cross-attention a to_kv row [k | k_diff | v]).
 template <int D>
-__global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restrict__ qkv, int64_t rs,
-                                                       const float* __restrict__ kw, const float* __restrict__ cosT,
+__global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restrict__ qkv, int64_t rs, int sk, int skd,
+                                                       int sv, const float* __restrict__ kw,
+                                                       const float* __restrict__ cosT,
                                                        const float* __restrict__ sinT, int half,
                                                        const float* __restrict__ vmask, int L, int Lp, int H,
                                                        float eps, int64_t region, uint16_t* __restrict__ ws) {
@@ -73,7 +76,7 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
     const uint16_t* row = qkv + (static_cast<int64_t>(b) * L + (l < L ? l : 0)) * rs + h * D;
 #pragma unroll
     for (int si = 0; si < 2; ++si) {
-      const int sec = 1 + 3 * si;  // k, k_diff
+      const int sec = si == 0 ? sk : skd;
       raw[i][si][0] = l < L ? ld16(row + sec * HD + 8 * tm1[i]) : u32x4{0u, 0u, 0u, 0u};
       raw[i][si][1] = l < L ? ld16(row + sec * HD + 8 * tm2[i]) : u32x4{0u, 0u, 0u, 0u};
     }
@@ -91,7 +94,7 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
 #pragma unroll
   for (int i = 0; i < VCH; ++i) {
     const int ch = t + 256 * i, l = l0 + ch / (D / 8), col = (ch % (D / 8)) * 8;
-    vraw[i] = l < L ? ld16(qkv + (static_cast<int64_t>(b) * L + l) * rs + 2 * HD + h * D + col)
+    vraw[i] = l < L ? ld16(qkv + (static_cast<int64_t>(b) * L + l) * rs + sv * HD + h * D + col)
                     : u32x4{0u, 0u, 0u, 0u};
     vm[i] = l < L ? (vmask ? vmask[static_cast<int64_t>(b) * L + l] : 1.f) : 0.f;
   }
@@ -281,12 +284,14 @@ __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, con
   }
 }
 
+// `qkv` rows hold q at section 0 and q_diff at section `sqd` (units of H * D); the L queries are padded to Lp (a
+// multiple of 128), the Lk keys of the workspace to Lkp. Self-attention has Lk = L.
 template <int D>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
-    const uint16_t* __restrict__ qkv, int64_t rs, const float* __restrict__ cosT, const float* __restrict__ sinT,
-    int half, float eps, const uint16_t* __restrict__ ws, int64_t region, int B, int L, int Lp, int H,
-    const float* __restrict__ qw, const float* __restrict__ kw, const float* __restrict__ lam,
-    uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ qkv, int64_t rs, int sqd, const float* __restrict__ cosT,
+    const float* __restrict__ sinT, int half, float eps, const uint16_t* __restrict__ ws, int64_t region, int B,
+    int L, int Lp, int Lk, int Lkp, int H, const float* __restrict__ qw, const float* __restrict__ kw,
+    const float* __restrict__ lam, uint16_t* __restrict__ out) {
   using T = DenseTile<D>;
   constexpr int NB = T::NB, NCT = T::NCT;
   // Stages A and B of the K/V tiles; the epilogue reuses the first 32 KB as its exchange buffer.
@@ -297,7 +302,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
   const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
   const int br0 = T::SPLIT ? wave >> 1 : 0;                          // first branch of this wave
   const int q0 = qb * 128 + (T::SPLIT ? (wave & 1) * 64 : wave * 32);  // first query of this wave
-  const int64_t rowbase = static_cast<int64_t>(bh) * Lp;
+  const int64_t rowbase = static_cast<int64_t>(bh) * Lkp;
 
   // Launch-uniform choice between the max-free and the running-max softmax (see the file comment).
   const SoftmaxPlan plan = dense_plan<D>(qw, kw);
@@ -310,7 +315,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
   {
     const int64_t HD = static_cast<int64_t>(H) * D;
     const int qrow = T::SPLIT ? q0 + lane : q0 + lr;
-    const int sec = 3 * (T::SPLIT ? br0 : lh);  // q is section 0 of a qkv row, q_diff section 3
+    const int sec = (T::SPLIT ? br0 : lh) ? sqd : 0;
     const int qc = qrow < L ? qrow : L - 1;
     const uint16_t* row = qkv + (static_cast<int64_t>(b) * L + qc) * rs + sec * HD + h * D;
     const float* cs = cosT + static_cast<int64_t>(qc) * half;
@@ -363,9 +368,9 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void dense_attend_bf16(
   const TileCopy<D> copy(ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D);
   copy(0, lds_addr(smem));
   if (plan.fast)
-    dense_attend_loop<D, true>(copy, L, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
+    dense_attend_loop<D, true>(copy, Lk, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
   else
-    dense_attend_loop<D, false>(copy, L, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
+    dense_attend_loop<D, false>(copy, Lk, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
 
   // Both stages are free once every wave is past its last tile; the exchange reuses them.
   static_assert(2 * NCT * (D / 32) * 16 * 64 * 4 <= 2 * T::STAGE * 2, "exchange buffer exceeds the two stages");
@@ -430,6 +435,47 @@ static int dense_checks(const void* qkv, int dtype, int64_t row_stride, const fl
   return HB_OK;
 }
 
+namespace hb {
+
+int launch_dense_prep_bf16(hipStream_t stream, const void* kv, int64_t rs, int sk, int skd, int sv, const float* kw,
+                           const float* cos, const float* sin, int half, const float* vmask, int B, int Lk, int H,
+                           int D, float eps, const DenseLayout& lay, void* workspace) {
+  const dim3 grid(static_cast<unsigned>(lay.Lp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
+  const uint16_t* x = static_cast<const uint16_t*>(kv);
+  uint16_t* ws = static_cast<uint16_t*>(workspace);
+  const int Lkp = static_cast<int>(lay.Lp);
+  if (D == 64)
+    hipLaunchKernelGGL(dense_prep_bf16<64>, grid, dim3(256), 0, stream, x, rs, sk, skd, sv, kw, cos, sin, half, vmask,
+                       Lk, Lkp, H, eps, lay.region_elems, ws);
+  else
+    hipLaunchKernelGGL(dense_prep_bf16<128>, grid, dim3(256), 0, stream, x, rs, sk, skd, sv, kw, cos, sin, half,
+                       vmask, Lk, Lkp, H, eps, lay.region_elems, ws);
+  return launch_status("dense_prep");
+}
+
+int launch_dense_attend_bf16(hipStream_t stream, const void* q, int64_t rs, int sqd, const float* qw, const float* kw,
+                             const float* cos, const float* sin, int half, float eps, const float* lam, void* out,
+                             int B, int L, int Lk, int H, int D, const DenseLayout& lay, const void* workspace) {
+  const int Lp = (L + 127) / 128 * 128;
+  const int nblocks = B * H * (Lp / 128);
+  const uint16_t* x = static_cast<const uint16_t*>(q);
+  const uint16_t* ws = static_cast<const uint16_t*>(workspace);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  const int Lkp = static_cast<int>(lay.Lp);
+  if (D == 64)
+    hipLaunchKernelGGL(dense_attend_bf16<64>, dim3(nblocks), dim3(DenseTile<64>::NT), 0, stream, x, rs, sqd, cos, sin,
+                       half, eps, ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw, lam, o);
+  else
+    hipLaunchKernelGGL(dense_attend_bf16<128>, dim3(nblocks), dim3(DenseTile<128>::NT), 0, stream, x, rs, sqd, cos,
+                       sin, half, eps, ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw, lam, o);
+  return launch_status("dense_attend");
+}
+
+}  // namespace hb
+
+// Sections of a to_qkv row [q | k | v | q_diff | k_diff] (dit.py:196-198), in units of H * D.
+constexpr int kSecK = 1, kSecV = 2, kSecQd = 3, kSecKd = 4;
+
 extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride, const float* q_weight,
                              const float* k_weight, const float* cos, const float* sin, int half, const float* vmask,
                              int B, int L, int H, int D, float eps, void* workspace, size_t workspace_bytes) {
@@ -438,19 +484,10 @@ extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int
                               workspace_bytes, lay);
   if (st) return st;
   if (dtype == HB_F32)
-    return launch_dense_prep_f32(stream, qkv, row_stride, k_weight, cos, sin, half, vmask, B, L, H, D, eps, lay,
-                                 workspace);
-  const dim3 grid(static_cast<unsigned>(lay.Lp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
-  const uint16_t* x = static_cast<const uint16_t*>(qkv);
-  uint16_t* ws = static_cast<uint16_t*>(workspace);
-  const int Lp = static_cast<int>(lay.Lp);
-  if (D == 64)
-    hipLaunchKernelGGL(dense_prep_bf16<64>, grid, dim3(256), 0, stream, x, row_stride, k_weight, cos, sin, half, vmask,
-                       L, Lp, H, eps, lay.region_elems, ws);
-  else
-    hipLaunchKernelGGL(dense_prep_bf16<128>, grid, dim3(256), 0, stream, x, row_stride, k_weight, cos, sin, half, vmask,
-                       L, Lp, H, eps, lay.region_elems, ws);
-  return launch_status("dense_prep");
+    return launch_dense_prep_f32(stream, qkv, row_stride, kSecK, kSecKd, kSecV, k_weight, cos, sin, half, vmask, B, L,
+                                 H, D, eps, lay, workspace);
+  return launch_dense_prep_bf16(stream, qkv, row_stride, kSecK, kSecKd, kSecV, k_weight, cos, sin, half, vmask, B, L,
+                                H, D, eps, lay, workspace);
 }
 
 extern "C" int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
@@ -467,22 +504,12 @@ extern "C" int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, i
   if (st) return st;
   if (dtype == HB_F32) {
     if (reinterpret_cast<uintptr_t>(out) % 16) return fail(HB_ERR_STRIDE, "fp32 out must be 16-byte aligned");
-    return launch_dense_attend_f32(stream, qkv, row_stride, q_weight, cos, sin, half, eps, workspace, lam, out, B, L, H,
-                                   D, lay);
+    return launch_dense_attend_f32(stream, qkv, row_stride, kSecQd, q_weight, cos, sin, half, eps, workspace, lam, out,
+                                   B, L, L, H, D, lay);
   }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
-  const int nblocks = B * H * static_cast<int>(lay.Lp / 128);
-  const uint16_t* x = static_cast<const uint16_t*>(qkv);
-  const uint16_t* ws = static_cast<const uint16_t*>(workspace);
-  uint16_t* o = static_cast<uint16_t*>(out);
-  const int Lp = static_cast<int>(lay.Lp);
-  if (D == 64)
-    hipLaunchKernelGGL(dense_attend_bf16<64>, dim3(nblocks), dim3(DenseTile<64>::NT), 0, stream, x, row_stride, cos,
-                       sin, half, eps, ws, lay.region_elems, B, L, Lp, H, q_weight, k_weight, lam, o);
-  else
-    hipLaunchKernelGGL(dense_attend_bf16<128>, dim3(nblocks), dim3(DenseTile<128>::NT), 0, stream, x, row_stride, cos,
-                       sin, half, eps, ws, lay.region_elems, B, L, Lp, H, q_weight, k_weight, lam, o);
-  return launch_status("dense_attend");
+  return launch_dense_attend_bf16(stream, qkv, row_stride, kSecQd, q_weight, k_weight, cos, sin, half, eps, lam, out, B,
+                                  L, L, H, D, lay, workspace);
 }
 
 extern "C" int hb_dense_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,

@@ -125,8 +125,9 @@ __device__ __forceinline__ void store_diff_f32(float* __restrict__ smem, const f
 // head, all in fp32, into the workspace regions k', k_diff', v'. Thread task = (token, RoPE group pair) as in the
 // bf16 prep: the rotation partner of every dim is in the thread's own registers.
 template <int D>
-__global__ __launch_bounds__(256) void dense_prep_f32(const float* __restrict__ qkv, int64_t rs,
-                                                      const float* __restrict__ kw, const float* __restrict__ cosT,
+__global__ __launch_bounds__(256) void dense_prep_f32(const float* __restrict__ qkv, int64_t rs, int sk, int skd,
+                                                      int sv, const float* __restrict__ kw,
+                                                      const float* __restrict__ cosT,
                                                       const float* __restrict__ sinT,
                                                       int half, const float* __restrict__ vmask, int L, int Lp, int H,
                                                       float eps, int64_t region, float* __restrict__ ws) {
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(256) void dense_prep_f32(const float* __restrict__ 
     }
 #pragma unroll
     for (int si = 0; si < 2; ++si) {
-      const int sec = 1 + 3 * si;  // k, k_diff
+      const int sec = si == 0 ? sk : skd;
       const float* w = kw;
       float x1[8] = {}, x2[8] = {};
       if (in) {
@@ -199,7 +200,7 @@ __global__ __launch_bounds__(256) void dense_prep_f32(const float* __restrict__ 
     const int ch = t + 256 * i, key = ch / (D / 4), col = (ch % (D / 4)) * 4, l = l0 + key;
     f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
     if (l < L) {
-      v = ld4(qkv + (static_cast<int64_t>(b) * L + l) * rs + 2 * HD + h * D + col);
+      v = ld4(qkv + (static_cast<int64_t>(b) * L + l) * rs + sv * HD + h * D + col);
       v *= vmask ? vmask[static_cast<int64_t>(b) * L + l] : 1.f;
     }
     st4(ws + 2 * region + (bh * Lp + l) * D + col, v);
@@ -207,12 +208,12 @@ __global__ __launch_bounds__(256) void dense_prep_f32(const float* __restrict__ 
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict__ qkv, int64_t rs,
+__global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict__ qkv, int64_t rs, int sqd,
                                                         const float* __restrict__ qw, const float* __restrict__ cosT,
                                                         const float* __restrict__ sinT, int half, float eps,
                                                         const float* __restrict__ ws, int64_t region, int B, int L,
-                                                        int Lp, int H, const float* __restrict__ lam,
-                                                        float* __restrict__ out) {
+                                                        int Lp, int Lk, int Lkp, int H,
+                                                        const float* __restrict__ lam, float* __restrict__ out) {
   using T = F32Tile<D>;
   __shared__ __attribute__((aligned(16))) float smem[T::LDS_FLOATS];
   const int nqb = Lp / 64;
@@ -220,15 +221,15 @@ __global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict_
   const int qb = tile % nqb, bh = tile / nqb, h = bh % H, b = bh / H;
   const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
   const int br = wave >> 1, q0 = qb * 64 + (wave & 1) * 32;
-  const int64_t rowbase = static_cast<int64_t>(bh) * Lp;
+  const int64_t rowbase = static_cast<int64_t>(bh) * Lkp;
 
   // RMSNorm (dit.py:45-57) and rotate-half RoPE (dit.py:90-98) of this lane's half row (dims lh D/2 ..) of q
-  // (branch 1, section 0) or q_diff (branch 2, section 3), from qkv; the RoPE partner (d +- half) of each group of
-  // 4 dims is loaded directly. Rows at or past L give zeros.
+  // (branch 1, section 0) or q_diff (branch 2, section sqd), from qkv; the RoPE partner (d +- half) of each group
+  // of 4 dims is loaded directly. Rows at or past L give zeros.
   float qreg[D / 2];
   {
     const int q = q0 + lr, qc = q < L ? q : L - 1, h4 = half / 4;
-    const float* row = qkv + (static_cast<int64_t>(b) * L + qc) * rs + static_cast<int64_t>(3 * br) * H * D + h * D;
+    const float* row = qkv + (static_cast<int64_t>(b) * L + qc) * rs + static_cast<int64_t>(br ? sqd : 0) * H * D + h * D;
     float xp[D / 2];
     float ss = 0.f;
 #pragma unroll
@@ -268,9 +269,9 @@ __global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict_
   const float c = kLog2e / sqrtf(static_cast<float>(D));
 
   const float* src[3] = {ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D};
-  const int nkt = (L + 63) / 64;
+  const int nkt = (Lk + 63) / 64;
   for (int t = 0; t < nkt; ++t) {
-    // 3 tensors x 64 rows x D floats; rows past L are the zero padding of the workspace (t * 64 + 63 < Lp)
+    // 3 tensors x 64 rows x D floats; rows past Lk are the zero padding of the workspace (t * 64 + 63 < Lkp)
 #pragma unroll
     for (int s3 = 0; s3 < 3; ++s3)
 #pragma unroll
@@ -281,7 +282,7 @@ __global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict_
     __syncthreads();
     const int k0 = t * 64;
     attend_tile_f32<D>(smem + br * T::TILE, smem + 2 * T::TILE, qreg, o, lsum, m, c,
-                       [&](int k) { return k0 + k < L; });
+                       [&](int k) { return k0 + k < Lk; });
     __syncthreads();
   }
   const int q = q0 + lr;
@@ -405,36 +406,37 @@ static int launched(const char* what) {
   return HB_OK;
 }
 
-int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* kw, const float* cosT,
-                          const float* sinT, int half, const float* vmask, int B, int L, int H, int D, float eps,
-                          const DenseLayout& lay, void* ws) {
+int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, int sk, int skd, int sv, const float* kw,
+                          const float* cosT, const float* sinT, int half, const float* vmask, int B, int L, int H, int D,
+                          float eps, const DenseLayout& lay, void* ws) {
   const dim3 grid(static_cast<unsigned>(lay.Lp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
   const float* x = static_cast<const float*>(qkv);
   float* w = static_cast<float*>(ws);
   const int Lp = static_cast<int>(lay.Lp);
   if (D == 64)
-    hipLaunchKernelGGL(dense_prep_f32<64>, grid, dim3(256), 0, stream, x, rs, kw, cosT, sinT, half, vmask, L, Lp, H,
-                       eps, lay.region_elems, w);
+    hipLaunchKernelGGL(dense_prep_f32<64>, grid, dim3(256), 0, stream, x, rs, sk, skd, sv, kw, cosT, sinT, half, vmask,
+                       L, Lp, H, eps, lay.region_elems, w);
   else
-    hipLaunchKernelGGL(dense_prep_f32<128>, grid, dim3(256), 0, stream, x, rs, kw, cosT, sinT, half, vmask, L, Lp, H,
-                       eps, lay.region_elems, w);
+    hipLaunchKernelGGL(dense_prep_f32<128>, grid, dim3(256), 0, stream, x, rs, sk, skd, sv, kw, cosT, sinT, half,
+                       vmask, L, Lp, H, eps, lay.region_elems, w);
   return launched("dense_prep_f32");
 }
 
-int launch_dense_attend_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qw, const float* cosT,
-                            const float* sinT, int half, float eps, const void* ws, const float* lam, void* out, int B,
-                            int L, int H, int D, const DenseLayout& lay) {
-  const int nblocks = B * H * static_cast<int>(lay.Lp / 64);
+int launch_dense_attend_f32(hipStream_t stream, const void* qkv, int64_t rs, int sqd, const float* qw,
+                            const float* cosT, const float* sinT, int half, float eps, const void* ws, const float* lam,
+                            void* out, int B, int L, int Lk, int H, int D, const DenseLayout& lay) {
+  const int Lp = (L + 127) / 128 * 128;
+  const int nblocks = B * H * (Lp / 64);
   const float* x = static_cast<const float*>(qkv);
   const float* w = static_cast<const float*>(ws);
   float* o = static_cast<float*>(out);
-  const int Lp = static_cast<int>(lay.Lp);
+  const int Lkp = static_cast<int>(lay.Lp);
   if (D == 64)
-    hipLaunchKernelGGL(dense_attend_f32<64>, dim3(nblocks), dim3(256), 0, stream, x, rs, qw, cosT, sinT, half, eps, w,
-                       lay.region_elems, B, L, Lp, H, lam, o);
+    hipLaunchKernelGGL(dense_attend_f32<64>, dim3(nblocks), dim3(256), 0, stream, x, rs, sqd, qw, cosT, sinT, half, eps,
+                       w, lay.region_elems, B, L, Lp, Lk, Lkp, H, lam, o);
   else
-    hipLaunchKernelGGL(dense_attend_f32<128>, dim3(nblocks), dim3(256), 0, stream, x, rs, qw, cosT, sinT, half, eps, w,
-                       lay.region_elems, B, L, Lp, H, lam, o);
+    hipLaunchKernelGGL(dense_attend_f32<128>, dim3(nblocks), dim3(256), 0, stream, x, rs, sqd, qw, cosT, sinT, half,
+                       eps, w, lay.region_elems, B, L, Lp, Lk, Lkp, H, lam, o);
   return launched("dense_attend_f32");
 }
 

@@ -1,13 +1,16 @@
-"""The DiT self-attention call site with the `attention="hip"` dispatch (sa3jax/dit.py:179-200) and the
-per-clip table preparation it reads (sa3jax/dit.py:317-336).
+"""The DiT attention call sites with the `attention="hip"` dispatch: self-attention (sa3jax/dit.py:179-200) with
+the per-clip tables it reads (sa3jax/dit.py:317-336), and cross-attention (sa3jax/dit.py:203-215) with its context
+K/V hoisted out of the sampler loop (sa3jax/dit.py:274-284).
 
-Only the attention step of a DiT block is here: `to_qkv` -> differential self-attention -> `to_out`. The
-rest of the block (adaLN, cross-attention, feed-forward) is outside this package.
+Only the attention steps of a DiT block are here: `to_qkv` -> differential self-attention -> `to_out`, and
+`to_q` -> differential cross-attention against the prepared context -> `to_out`. The rest of the block (adaLN,
+feed-forward) is outside this package.
 """
 from __future__ import annotations
 
 import torch
 
+from hummingbird_amd import cross_attention as xattn
 from hummingbird_amd import dense_attention, xla_chain
 from hummingbird_amd.config import DiTConfig
 
@@ -54,4 +57,37 @@ def self_attention(h: torch.Tensor, block: dict, static: dict, cfg: DiTConfig,
             raise NotImplementedError("only the differential self-attention is on this package's path")
         out = xla_chain.dense_chain(qkv, attn["q_norm"]["weight"], attn["k_norm"]["weight"], static["inv_freq"],
                                     static["valid"], cfg.num_heads, cfg.head_dim, cfg.qk_norm_eps, lam=lam)
+    return out @ attn["to_out"]["weight"].t()
+
+
+def cross_context(block: dict, ctx: torch.Tensor, cfg: DiTConfig):
+    """The context's K/V for one block, computed once per clip (reference: dit._cross_kv, dit.py:274-284):
+    `to_kv` -> split -> k_norm on k and k_diff. With `attention="hip"` the result is a prepared
+    `cross_attention.CrossKV` on the device, otherwise the `(k, k_diff, v)` tensors of the XLA chain.
+    `block["cross_attn"]` holds `to_kv.weight (3E, C)`, `to_q.weight (2E, E)`, `to_out.weight (E, E)`,
+    `q_norm.weight`, `k_norm.weight`."""
+    attn = block["cross_attn"]
+    kv = ctx @ attn["to_kv"]["weight"].t()
+    if use_hip(cfg, kv):
+        return xattn.prepare_cross_kv(kv, attn["k_norm"]["weight"], cfg.num_heads, cfg.head_dim, cfg.qk_norm_eps)
+    if not cfg.differential:
+        raise NotImplementedError("only the differential cross-attention is on this package's path")
+    return xla_chain.cross_kv(kv, attn["k_norm"]["weight"], cfg.num_heads, cfg.head_dim, cfg.qk_norm_eps)
+
+
+def cross_attention(h: torch.Tensor, block: dict, context, cfg: DiTConfig,
+                    lam: torch.Tensor | None = None) -> torch.Tensor:
+    """`to_q` -> differential cross-attention -> `to_out` (reference: dit._cross_attention, dit.py:203-215)
+    against `cross_context(...)` of the same block."""
+    attn = block["cross_attn"]
+    q = h @ attn["to_q"]["weight"].t()
+    if use_hip(cfg, q):
+        if not isinstance(context, xattn.CrossKV):
+            raise TypeError('attention="hip" needs the context prepared by cross_context with attention="hip"')
+        out = xattn.cross_attention(q, context, attn["q_norm"]["weight"], cfg.qk_norm_eps, lam=lam)
+    else:
+        if not cfg.differential:
+            raise NotImplementedError("only the differential cross-attention is on this package's path")
+        out = xla_chain.cross_chain(q, context, attn["q_norm"]["weight"], cfg.num_heads, cfg.head_dim,
+                                    cfg.qk_norm_eps, lam=lam)
     return out @ attn["to_out"]["weight"].t()

@@ -6,7 +6,9 @@ half-width `half` (default D/2) with inv_freq_i = 10000^(-2i/(2*half)); per-head
 mask of ones with the last `mask_tail` tokens of every row zeroed (or a ragged tail of 0-25 % per row).
 Band (SAME-L): qkv ~ N(0,1) `(B, S, 5*H*D)`; DyT alpha = 0.5, gamma ~ 1 + N(0, 0.02), beta ~ N(0, 0.02) for q and
 for k; the same RoPE and lambda recipe.
-Draw order: qkv, q-gain (or q DyT), k-gain (or k DyT), lambda, mask.
+Cross (DiT cross-attention): the block's to_q output ~ N(0,1) `(B, L, 2*H*D)`, the context's to_kv output
+~ N(0,1) `(B, Nk, 3*H*D)`, q/k RMSNorm gains and lambda as for dense.
+Draw order: qkv (cross: q, then kv), q-gain (or q DyT), k-gain (or k DyT), lambda, mask.
 """
 from __future__ import annotations
 
@@ -15,7 +17,8 @@ import numpy as np
 # The measured configurations (sizes from the workload definitions the benchmark reports against).
 DENSE_120S = dict(batch=2, length=2584, heads=24, head_dim=64)      # DiT at a 120 s clip, CFG batch 2
 BAND_120S = dict(batch=1, length=82688, heads=8, head_dim=64, window=128)  # SAME-L decoder at 120 s
-DENSE_CALLS_PER_CLIP = 192  # 8 sampler steps x 24 DiT blocks
+CROSS_120S = dict(batch=2, length=2584, context=257, heads=24, head_dim=64)  # DiT cross-attention, 257 tokens
+DENSE_CALLS_PER_CLIP = 192  # 8 sampler steps x 24 DiT blocks (the cross-attention calls as many times)
 BAND_CALLS_PER_CLIP = 12    # 12 SAME-L decoder blocks
 
 
@@ -75,6 +78,26 @@ def band_inputs(batch: int, length: int, heads: int, head_dim: int, window: int,
     lam = rng.uniform(0.2, 0.8, heads).astype(np.float32)
     return dict(qkv=qkv, q_norm=q_norm, k_norm=k_norm, inv_freq=inv_freq(half), lam=lam, heads=heads,
                 head_dim=head_dim, half=half, window=window)
+
+
+def cross_inputs(batch: int, length: int, context: int, heads: int, head_dim: int, seed: int = 0,
+                 dtype: str = "bf16", gain_std: float = 0.02, gain_mean: float = 1.0) -> dict:
+    """Cross-attention inputs as float32 NumPy arrays (q and kv hold bf16 values when dtype == 'bf16')."""
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((batch, length, 2 * heads * head_dim), dtype=np.float32)
+    kv = rng.standard_normal((batch, context, 3 * heads * head_dim), dtype=np.float32)
+    if dtype == "bf16":
+        q, kv = _bf16(q), _bf16(kv)
+    q_weight = (gain_mean + gain_std * rng.standard_normal(head_dim)).astype(np.float32)
+    k_weight = (gain_mean + gain_std * rng.standard_normal(head_dim)).astype(np.float32)
+    lam = rng.uniform(0.2, 0.8, heads).astype(np.float32)
+    return dict(q=q, kv=kv, q_weight=q_weight, k_weight=k_weight, lam=lam, heads=heads, head_dim=head_dim,
+                eps=1e-6)
+
+
+def cross_flops(batch: int, length: int, context: int, heads: int, head_dim: int) -> float:
+    """Algorithmic FLOPs of one cross-attention call: 2 branches x (QK^T + PV) x 2 flops per MAC."""
+    return 8.0 * batch * heads * length * context * head_dim
 
 
 def dense_flops(batch: int, length: int, heads: int, head_dim: int) -> float:

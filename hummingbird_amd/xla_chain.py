@@ -1,7 +1,8 @@
 """The reference's plain (non-kernel) attention chains, restated in torch for `attention="xla"`.
 
 These run wherever torch runs and keep the reference's cast points: bf16 logits, weights and subtraction for
-the DiT chain (sa3jax/dit.py:113-119, 131-176), fp32 DyT/RoPE/softmax/subtraction for the SAME-L chain
+the DiT self- and cross-attention chains (sa3jax/dit.py:113-119, 131-176, 203-215, 274-284), fp32
+DyT/RoPE/softmax/subtraction for the SAME-L chain
 (sa3jax/same_l.py:58-69, 92-100, 134-169). They are what `attention="xla"` selects; the `"hip"` path never
 falls back to them.
 """
@@ -50,6 +51,16 @@ def merge(x: torch.Tensor) -> torch.Tensor:
     return x.permute(0, 2, 1, 3).reshape(b, n, h * d)
 
 
+def sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, dtype: torch.dtype) -> torch.Tensor:
+    """One head's SDPA with the DiT chain's cast points (sa3jax/dit.py:113-119): logits formed in fp32 and
+    rounded to the compute dtype (as XLA's einsum does), scaled in that dtype, fp32 softmax, weights and PV in
+    the compute dtype."""
+    logits = (q.to(F32) @ k.to(F32).transpose(-1, -2)).to(dtype)
+    logits = (logits.to(F32) * scale).to(dtype)
+    weights = torch.softmax(logits.to(F32), dim=-1).to(dtype)
+    return (weights.to(F32) @ v.to(F32)).to(dtype)
+
+
 def dense_chain(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tensor, inv_freq: torch.Tensor,
                 valid: torch.Tensor | None, num_heads: int, head_dim: int, eps: float,
                 lam: torch.Tensor | None = None) -> torch.Tensor:
@@ -64,22 +75,40 @@ def dense_chain(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.Tenso
     q, k, qd, kd = (rope(t, cos, sin, dtype) for t in (q, k, qd, kd))
     if valid is not None:
         v = v * valid.to(dtype)[:, None, :, None]
+    return _subtract(q, k, v, qd, kd, head_dim, dtype, lam)
+
+
+def _subtract(q, k, v, qd, kd, head_dim: int, dtype: torch.dtype, lam: torch.Tensor | None) -> torch.Tensor:
+    """`SDPA(q, k, v) - lam * SDPA(q_diff, k_diff, v)` per head, cast once (sa3jax/dit.py:131-147)."""
+    num_heads = q.shape[1]
     scale = torch.tensor(1.0 / math.sqrt(head_dim), dtype=dtype).item()
-    lam_v = torch.ones(num_heads, dtype=F32, device=qkv.device) if lam is None else lam.to(F32)
-
-    def sdpa(qq, kk, vv):
-        logits = (qq.to(F32) @ kk.to(F32).transpose(-1, -2)).to(dtype)
-        logits = (logits.to(F32) * scale).to(dtype)
-        weights = torch.softmax(logits.to(F32), dim=-1).to(dtype)
-        return (weights.to(F32) @ vv.to(F32)).to(dtype)
-
+    lam_v = torch.ones(num_heads, dtype=F32, device=q.device) if lam is None else lam.to(F32)
     out = torch.empty_like(q)
     for b in range(q.shape[0]):
         for h in range(num_heads):
-            first = sdpa(q[b, h], k[b, h], v[b, h])
-            second = sdpa(qd[b, h], kd[b, h], v[b, h])
+            first = sdpa(q[b, h], k[b, h], v[b, h], scale, dtype)
+            second = sdpa(qd[b, h], kd[b, h], v[b, h], scale, dtype)
             out[b, h] = (first.to(F32) - lam_v[h] * second.to(F32)).to(dtype)
     return merge(out)
+
+
+def cross_kv(kv: torch.Tensor, k_weight: torch.Tensor, num_heads: int, head_dim: int,
+             eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The hoisted context K/V (sa3jax/dit.py:274-284): the `(B, Nk, 3*H*D)` to_kv output split into k, k_diff and
+    v, heads first; k and k_diff RMS-normed (dit.py:122-128), v as is."""
+    k, kd, v = (heads(t, num_heads, head_dim) for t in kv.split(num_heads * head_dim, dim=-1))
+    return rms(k, k_weight, eps), rms(kd, k_weight, eps), v
+
+
+def cross_chain(q_proj: torch.Tensor, context: tuple[torch.Tensor, torch.Tensor, torch.Tensor],
+                q_weight: torch.Tensor, num_heads: int, head_dim: int, eps: float,
+                lam: torch.Tensor | None = None) -> torch.Tensor:
+    """The DiT cross-attention chain (sa3jax/dit.py:203-215 -> 150-176 -> 131-147) for a `(B, L, 2*H*D)` to_q
+    output against `cross_kv(...)`: q and q_diff RMS-normed, no RoPE, no mask."""
+    q, qd = (heads(t, num_heads, head_dim) for t in q_proj.split(num_heads * head_dim, dim=-1))
+    q, qd = rms(q, q_weight, eps), rms(qd, q_weight, eps)
+    k, kd, v = context
+    return _subtract(q, k, v, qd, kd, head_dim, q_proj.dtype, lam)
 
 
 def dyt(x: torch.Tensor, alpha, gamma: torch.Tensor, beta: torch.Tensor) -> torch.Tensor:

@@ -1,11 +1,14 @@
 /* hummingbird_amd: MI355X (gfx950) differential-attention kernels behind a plain C ABI.
  *
- * Two operations replace the reference's two fused TPU kernels (kelechi-c/hummingbird, sa3jax/):
+ * Two operations replace the reference's two fused TPU kernels (kelechi-c/hummingbird, sa3jax/), and a third
+ * the DiT cross-attention chain next to them:
  *
  *   hb_dense_diffattn  replaces  dense_attention.dense_attention  (sa3jax/dense_attention.py:104-153),
  *                      called from dit._self_attention (sa3jax/dit.py:191-195);
  *   hb_band_diffattn   replaces  band_attention.band_attention    (sa3jax/band_attention.py:123-180),
  *                      called from same_l._attention (sa3jax/same_l.py:158-161);
+ *   hb_cross_prep +    replace   the XLA chain of dit._cross_attention and its hoisted context K/V
+ *   hb_cross_attend              (sa3jax/dit.py:203-215, 274-284), which the reference runs without a kernel;
  *   hb_rope_tables     replaces  band_attention.rope_tables / dit._rope_tables
  *                      (sa3jax/band_attention.py:43-58, sa3jax/dit.py:82-87) in a kernel-native layout.
  *
@@ -121,6 +124,31 @@ int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row
                      const float* q_dyt, const float* k_dyt, const float* cos, const float* sin, int half,
                      int window, const float* lam, void* out, int B, int S, int H, int D, void* workspace,
                      size_t workspace_bytes);
+
+/* ---- DiT differential cross-attention -------------------------------------------------------------------
+ * Replaces the XLA chain of dit._cross_attention (sa3jax/dit.py:203-215) with its hoisted context K/V
+ * (dit._cross_kv, sa3jax/dit.py:274-284). Per (batch b, head h):
+ *   q, q_diff <- RMSNorm(x; q_weight, eps) of the block's to_q output rows, q at section 0, q_diff at section 1
+ *                (a row is [q | q_diff], sa3jax/dit.py:207-209);
+ *   k, k_diff <- RMSNorm(x; k_weight, eps), v <- x, of the context's to_kv output rows (a row is
+ *                [k | k_diff | v], sa3jax/dit.py:279-281);
+ *   out = softmax(q k^T / sqrt(D)) v - lam[h] * softmax(q_diff k_diff^T / sqrt(D)) v   (sa3jax/dit.py:131-147),
+ * over all Nk context keys: no RoPE and no mask (sa3jax/dit.py:204-205, 214-215).
+ *   q      : (B, L, >= 2*H*D) with row stride `row_stride` (a multiple of 8), 16-byte aligned
+ *   kv     : (B, Nk, >= 3*H*D) with row stride `row_stride` (a multiple of 8), 16-byte aligned
+ *   dtype  : HB_BF16 or HB_F32 (of q, kv and out);  D: 64 or 128;  eps >= 0
+ *   workspace : >= hb_cross_workspace_size(dtype, B, Nk, H, D) bytes, 256-byte aligned.
+ * hb_cross_prep writes the prepared k, k_diff and v of the context into the workspace; hb_cross_attend reads
+ * them, for as many query sets as the caller has (the reference computes them once per clip and reuses them in
+ * every sampler step). k_weight is passed to hb_cross_attend too: it bounds the logits for the softmax. */
+size_t hb_cross_workspace_size(int dtype, int B, int Nk, int H, int D);
+int hb_cross_validate(int dtype, int64_t q_row_stride, int64_t kv_row_stride, int B, int L, int Nk, int H, int D,
+                      float eps);
+int hb_cross_prep(hipStream_t stream, const void* kv, int dtype, int64_t row_stride, const float* k_weight, int B,
+                  int Nk, int H, int D, float eps, void* workspace, size_t workspace_bytes);
+int hb_cross_attend(hipStream_t stream, const void* q, int dtype, int64_t row_stride, const float* q_weight,
+                    const float* k_weight, const float* lam, void* out, int B, int L, int Nk, int H, int D, float eps,
+                    const void* workspace, size_t workspace_bytes);
 
 #ifdef __cplusplus
 }
