@@ -37,16 +37,17 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   else return row * RL + 8 * (chunk ^ (row & 15));
 }
 
-// Attention tiling: a workgroup of 4 waves attends 128 queries. D = 64: each wave owns one differential branch
-// of 64 queries (two MFMA column tiles), so every K fragment read from LDS feeds two MFMAs while a wave's
-// registers still fit two waves per SIMD; waves 0-1 run branch 1 (q, k) and waves 2-3 branch 2 (q_diff,
-// k_diff), and the second pair hands its normalised result to the first through LDS at the end. D = 128: each
-// wave owns both branches of 32 queries.
-template <int D>
+// Attention tiling: a workgroup of 4 waves attends QB queries (128, or 64 for grids too small to fill the GPU).
+// D = 64: each wave owns one differential branch of QB / 2 queries (QB / 64 MFMA column tiles; at QB = 128 every
+// K fragment read from LDS feeds two MFMAs while a wave's registers still fit two waves per SIMD); waves 0-1 run
+// branch 1 (q, k) and waves 2-3 branch 2 (q_diff, k_diff), and the second pair hands its normalised result to the
+// first through LDS at the end. D = 128 (QB = 128 only): each wave owns both branches of 32 queries.
+template <int D, int QB = 128>
 struct DenseTile {
-  static constexpr bool SPLIT = D == 64;   // one branch per wave
-  static constexpr int NB = SPLIT ? 1 : 2;  // branches per wave
-  static constexpr int NCT = SPLIT ? 2 : 1; // 32-query column tiles per wave
+  static_assert(QB == 128 || (D == 64 && QB == 64), "64-query workgroups exist for head_dim 64 only");
+  static constexpr bool SPLIT = D == 64;          // one branch per wave
+  static constexpr int NB = SPLIT ? 1 : 2;         // branches per wave
+  static constexpr int NCT = SPLIT ? QB / 64 : 1;  // 32-query column tiles per wave
   static constexpr int NT = 256;            // threads per workgroup
   static constexpr int K_ELEMS = 64 * D;     // one tensor of a 64-key tile: K, K_diff [key][d]; V^T [d][pos]
   static constexpr int STAGE = 3 * K_ELEMS;  // K, K_diff, V^T of one 64-key tile, swizzled rows
@@ -90,18 +91,18 @@ struct TileCopy {
   }
 };
 
-// out[q, h*D + d] = O1 / l1 - lam * O2 / l2 for the 128 queries q0 .. q0 + 127 of a 4-wave workgroup laid out as
-// DenseTile<D> describes (q0w: this wave's first query, br0: its first branch), written as bf16 for q < N.
+// out[q, h*D + d] = O1 / l1 - lam * O2 / l2 for the QB queries of a 4-wave workgroup laid out as DenseTile<D, QB>
+// describes (q0w: this wave's first query, br0: its first branch), written as bf16 for q < N.
 // D = 64: the branch-2 waves publish lam * O2 / l2 (rounded per element) through LDS (`xbuf_mem`, at least
 // 32 KB, free of tile reads: the caller has passed a barrier after its last tile) and the branch-1 waves
 // subtract it from O1 / l1; D = 128: each wave holds both branches. Every lane of the workgroup must call it.
-template <int D>
+template <int D, int QB = 128>
 __device__ __forceinline__ void store_diff_split(uint16_t* __restrict__ out, int64_t b, int N, int H, int h, int q0w,
                                                  int br0, float lamh,
-                                                 const f32x16 (&o)[DenseTile<D>::NB][DenseTile<D>::NCT][D / 32],
-                                                 const float (&lsum)[DenseTile<D>::NB][DenseTile<D>::NCT],
+                                                 const f32x16 (&o)[DenseTile<D, QB>::NB][DenseTile<D, QB>::NCT][D / 32],
+                                                 const float (&lsum)[DenseTile<D, QB>::NB][DenseTile<D, QB>::NCT],
                                                  uint16_t* xbuf_mem) {
-  using T = DenseTile<D>;
+  using T = DenseTile<D, QB>;
   constexpr int NCT = T::NCT;
   const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
   const int64_t HD = static_cast<int64_t>(H) * D;

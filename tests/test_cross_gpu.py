@@ -123,6 +123,19 @@ def test_cross_120s_vs_torch_chain():
     assert_bf16_parity(got[-1, :, hh * D:(hh + 1) * D], oracle(head, "bf16")[0], "cross 120s last head vs oracle")
 
 
+def test_cross_reference_geometry_64_query_workgroups():
+    """The reference's own 120 s geometry (B=1, L=1422, 257 context tokens, 24 heads: 288 workgroups of 128
+    queries, run as 64-query workgroups) against the torch restatement."""
+    B, L, Nk, H, D = 1, 1422, 257, 24, 64
+    announce(f"cross bf16 reference geometry B={B} L={L} Nk={Nk} H={H}")
+    inp = workloads.cross_inputs(B, L, Nk, H, D, seed=8)
+    got = run_hip(inp)
+    context = xla_chain.cross_kv(dev(inp["kv"], torch.bfloat16), dev(inp["k_weight"]), H, D, inp["eps"])
+    ref = xla_chain.cross_chain(dev(inp["q"], torch.bfloat16), context, dev(inp["q_weight"]), H, D, inp["eps"],
+                                lam=dev(inp["lam"])).float().cpu().numpy()
+    assert_bf16_parity(got, ref, "cross reference geometry vs torch chain")
+
+
 def test_cross_caller_mirror_hip_vs_xla():
     """dit.cross_context + dit.cross_attention with attention="hip" against attention="xla" on the GPU (bf16):
     to_kv and to_q projections, the attention, to_out."""

@@ -170,6 +170,36 @@ def test_dense_120s_vs_torch_chain():
     assert_bf16_parity(got[1, :, h * 64:(h + 1) * 64], oracle(sub, "xla")[0], "120s head 5 vs oracle")
 
 
+BALANCED = [  # (B, L, H, half): 257 to 384 workgroups of 128 queries, where the 64-query workgroups run
+    (1, 1422, 24, 16), (2, 700, 24, 32), (1, 2000, 20, 8), (3, 513, 25, 24),
+]
+
+
+@pytest.mark.parametrize("shape", BALANCED, ids=lambda s: "B%dL%dH%dh%d" % s)
+def test_dense_64_query_workgroups_vs_torch_chain(shape):
+    """Grids of between one and one and a half 128-query workgroups per CU run 64-query workgroups (three per CU);
+    the first shape is the reference's own 120 s DiT geometry (B=1, L=1422 = 64 memory + 1358 latent tokens,
+    half=16). Checked against the torch restatement of the XLA chain, and the last head against the oracle."""
+    B, L, H, half = shape
+    blocks = B * H * -(-L // 128)
+    assert 256 < blocks <= 384, blocks
+    announce(f"dense bf16 64-query workgroups {shape} ({blocks} x 128 queries)")
+    inp = workloads.dense_inputs(B, L, H, 64, seed=L + H, half=half, ragged=True)
+    got = run_hip(inp)
+    qkv = torch.from_numpy(inp["qkv"]).to(DEV, torch.bfloat16)
+    ref = xla_chain.dense_chain(qkv, torch.from_numpy(inp["q_weight"]).to(DEV),
+                                torch.from_numpy(inp["k_weight"]).to(DEV), torch.from_numpy(inp["inv_freq"]).to(DEV),
+                                torch.from_numpy(inp["valid"]).to(DEV), H, 64, 1e-6,
+                                lam=torch.from_numpy(inp["lam"]).to(DEV)).float().cpu().numpy()
+    assert_bf16_parity(got, ref, f"{shape} vs torch chain")
+    h = H - 1
+    hd = H * 64
+    cols = np.concatenate([np.arange(sec * hd + h * 64, sec * hd + h * 64 + 64) for sec in range(5)])
+    sub = dict(inp, qkv=np.ascontiguousarray(inp["qkv"][-1:, :, cols]), heads=1, lam=inp["lam"][h:h + 1],
+               valid=inp["valid"][-1:])
+    assert_bf16_parity(got[-1, :, h * 64:(h + 1) * 64], oracle(sub, "xla")[0], f"{shape} last head vs oracle")
+
+
 def test_dense_380s_vs_torch_chain():
     """The 380 s clip shape (B=2, L=8180, 24 heads of 64): long-sequence accumulation over 128 key tiles, checked
     against the torch restatement of the XLA chain on the GPU (inputs drawn on the device)."""
