@@ -5,6 +5,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+
 namespace hb {
 
 namespace {
@@ -29,6 +31,21 @@ DenseLayout dense_layout(int dtype, int B, int L, int H, int D) {
   lay.region_bytes = static_cast<size_t>(lay.region_elems) * lay.elem_bytes;
   lay.total_bytes = 3 * lay.region_bytes;
   return lay;
+}
+
+int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];  // zero-initialised (static storage); 0 = not yet queried
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  if (dev < kMaxDevices) {
+    const int n = cached[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < kMaxDevices) cached[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int half) {

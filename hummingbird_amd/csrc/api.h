@@ -32,6 +32,8 @@ struct DenseLayout {
 DenseLayout dense_layout(int dtype, int B, int L, int H, int D);
 
 int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int half);
+// Multiprocessor (CU) count of the current device, queried once per device (256 if the query fails).
+int device_cus();
 
 // Dense kernels (dense.hip: bf16, fp32.hip: fp32). Arguments are validated by the exported entry points before
 // these are called. The prep reads k, k_diff and v from sections sk, skd and sv of the rows of `kv` (units of

@@ -517,14 +517,7 @@ int launch_band_ring(hipStream_t stream, const void* qkv, int64_t rs, const floa
                      const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                      int S, int H) {
   using namespace band_ring;
-  static int cu_count[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
-  int ncu = dev < 64 ? cu_count[dev] : 0;
-  if (ncu <= 0) {
-    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0) ncu = 256;
-    if (dev < 64) cu_count[dev] = ncu;
-  }
+  const int ncu = device_cus();
   Args a;
   a.qkv = static_cast<const uint16_t*>(qkv);
   a.rs = rs;

@@ -457,18 +457,6 @@ int launch_dense_prep_bf16(hipStream_t stream, const void* kv, int64_t rs, int s
   return launch_status("dense_prep");
 }
 
-// Multiprocessor count of the current device (cached per device).
-static int device_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-  if (dev < 64) cached[dev] = n;
-  return n;
-}
-
 int launch_dense_attend_bf16(hipStream_t stream, const void* q, int64_t rs, int sqd, const float* qw, const float* kw,
                              const float* cos, const float* sin, int half, float eps, const float* lam, void* out,
                              int B, int L, int Lk, int H, int D, const DenseLayout& lay, const void* workspace) {
