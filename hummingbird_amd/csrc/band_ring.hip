@@ -400,9 +400,11 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
       // The wave's tiles form one contiguous range of the ring; the scores of tile i + 1 are issued on the
       // matrix core before the softmax of tile i, so the two overlap.
       const int ilo = (ulo >> 6) - (j - C), ihi = (uhi >> 6) - (j - C);
+      // The wave's tiles span at most RING consecutive slots, starting at the slot of tile ilo.
+      const int kt0 = j - C + ilo, slot0 = (kt0 % RING + RING) % RING;
       auto tile_ptr = [&](int i) {
-        const int kt = j - C + i;
-        return ring + ((kt % RING + RING) % RING) * TILE;
+        const int sl = slot0 + (i - ilo);
+        return ring + (sl >= RING ? sl - RING : sl) * TILE;
       };
       // 32-key half rt of tile i takes part: it meets the band of at least one query of the wave.
       auto active = [&](int i, int rt) {
@@ -450,22 +452,27 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
       // of d-tile 0).
       const float inv = __frcp_rn(lsum + __shfl_xor(lsum, 32, kWave));
       const float li = br == 1 ? __fmul_rn(lamh, inv) : inv;  // this branch's factor
-      float* xs = xbuf + qhalf * (2 * 16 * 64);                // [d-tile][register][lane]
-      const int give = 1 - br;                                 // the d-tile the other wave stores
+      f32x4* xs = reinterpret_cast<f32x4*>(xbuf) + qhalf * (2 * 4 * 64);  // [d-tile][register / 4][lane][4]
+      const int give = 1 - br;                                           // the d-tile the other wave stores
 #pragma unroll
-      for (int r = 0; r < 16; ++r) xs[(give * 16 + r) * 64 + lane] = __fmul_rn(o[give][r], li);
+      for (int g = 0; g < 4; ++g) {
+        f32x4 v;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) v[jj] = __fmul_rn(o[give][4 * g + jj], li);
+        xs[(give * 4 + g) * 64 + lane] = v;
+      }
       __syncthreads();
       {
         const int dt = br;  // the d-tile this wave stores
         uint16_t* orow = a.out + (static_cast<int64_t>(b) * S + q) * HD + h * D + 32 * dt;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
+          const f32x4 other = xs[(dt * 4 + g) * 64 + lane];
           float v[4];
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            const int r = 4 * g + jj;
-            const float mine = __fmul_rn(o[dt][r], li), other = xs[(dt * 16 + r) * 64 + lane];
-            v[jj] = br == 0 ? __fsub_rn(mine, other) : __fsub_rn(other, mine);
+            const float mine = __fmul_rn(o[dt][4 * g + jj], li);
+            v[jj] = br == 0 ? __fsub_rn(mine, other[jj]) : __fsub_rn(other[jj], mine);
           }
           if (q < S) {
             u32x2 pk;
