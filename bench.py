@@ -130,8 +130,9 @@ EXTRA_BAND = {"ref_true_120s": (1, 23086, 24, 64, 17, 16), "clip_380s": (1, 2617
 
 
 def extra_shapes(lib, sp, stream, dev) -> dict:
-    """Per-call p10/p50/p90 and roofline fractions of the dense and band calls at the extra shapes, and of the DiT
-    cross-attention at the 120 s clip (synthetic N(0,1) inputs drawn on the device, unit gains, lam = 1)."""
+    """Per-call p10/p50/p90 and roofline fractions of the dense and band calls at the extra shapes, of the DiT
+    cross-attention and of a SAME-L decoder block at the 120 s clip (synthetic N(0,1) inputs drawn on the device,
+    unit gains, lam = 1)."""
     import torch
 
     from hummingbird_amd import _lib
@@ -202,7 +203,56 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
                          "mfma_frac_p50": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
                          "ms_per_clip": round(wl.DENSE_CALLS_PER_CLIP * pc["p50"] / 1e3, 3)}
     del q, kv, ws, out
+    res["same_l_block_120s"] = block_shape(lib, sp, stream, dev, gen)
     return res
+
+
+def block_shape(lib, sp, stream, dev, gen) -> dict:
+    """One SAME-L decoder block at the 120 s clip (S=82688 frames, dim 512 = 8 heads of 64, ff 1536, w=128):
+    hb_dyt and hb_glu per call with their HBM fractions, and the whole block (DyT -> to_qkv -> band attention ->
+    to_out -> residual -> DyT -> glu_proj -> GLU -> proj_out -> residual; GEMMs on torch/hipBLASLt)."""
+    import torch
+
+    from hummingbird_amd import _lib, same_l
+    from hummingbird_amd import workloads as wl
+    from hummingbird_amd.config import SameConfig
+
+    S, dim, ff = wl.BAND_120S["length"], 8 * 64, 8 * 64 * 3
+    x = torch.randn((1, S, dim), device=dev, generator=gen).to(torch.bfloat16)
+    dyt = torch.cat([torch.tensor([0.5], device=dev), torch.ones(dim, device=dev), torch.zeros(dim, device=dev)])
+    y = torch.empty_like(x)
+    proj = torch.randn((1, S, 2 * ff), device=dev, generator=gen).to(torch.bfloat16)
+    g = torch.empty((1, S, ff), dtype=torch.bfloat16, device=dev)
+    bias = torch.zeros(2 * ff, device=dev)
+
+    def dyt_call():
+        _lib.check(lib.hb_dyt(sp, x.data_ptr(), _lib.HB_BF16, dim, dyt.data_ptr(), y.data_ptr(), dim, S, dim), "dyt")
+
+    def glu_call():
+        _lib.check(lib.hb_glu(sp, proj.data_ptr(), _lib.HB_BF16, 2 * ff, bias.data_ptr(), 1, g.data_ptr(), ff, S, ff),
+                   "glu")
+    pd, pg = call_percentiles(dyt_call, 20, stream), call_percentiles(glu_call, 20, stream)
+    dyt_bytes, glu_bytes = 2.0 * S * dim * 2, float(S) * 3 * ff * 2
+
+    def w(o, i):
+        return (torch.randn((o, i), device=dev, generator=gen) / i ** 0.5).to(torch.bfloat16)
+
+    def norm(c):
+        return {"alpha": torch.tensor(0.5, device=dev), "gamma": torch.ones(c, device=dev),
+                "beta": torch.zeros(c, device=dev)}
+    params = {"pre_norm": norm(dim), "ff_norm": norm(dim),
+              "rope_inv_freq": torch.from_numpy(wl.inv_freq(32)).to(dev),
+              "self_attn": {"to_qkv": {"weight": w(5 * dim, dim)}, "to_out": {"weight": w(dim, dim)},
+                            "q_norm": norm(64), "k_norm": norm(64)},
+              "ff": {"glu_proj": {"weight": w(2 * ff, dim), "bias": torch.zeros(2 * ff, device=dev, dtype=torch.bfloat16)},
+                     "proj_out": {"weight": w(dim, ff), "bias": torch.zeros(dim, device=dev, dtype=torch.bfloat16)}}}
+    cfg = SameConfig(channels=128, c_mults=(4,), stride=127, transformer_depth=12, sinusoidal_blocks=8,
+                     attention="hip")  # dim 512, half-width 128
+    pb = call_percentiles(lambda: same_l.block(x, params, 11, cfg), 10, stream)
+    return {"shape": {"S": S, "dim": dim, "ff": ff, "w": cfg.sub_chunk_size},
+            "dyt_us_per_call": pd, "dyt_hbm_frac_p50": round(dyt_bytes / (pd["p50"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "glu_us_per_call": pg, "glu_hbm_frac_p50": round(glu_bytes / (pg["p50"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "block_us_per_call": pb}
 
 
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA

@@ -45,6 +45,8 @@ SIGNATURES = {
                               c_void_p, c_size_t]),
     "hb_cross_attend": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                 c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t]),
+    "hb_dyt": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int]),
+    "hb_glu": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int, c_void_p, c_int64, c_int64, c_int]),
 }
 
 _lib: ctypes.CDLL | None = None

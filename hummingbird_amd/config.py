@@ -44,8 +44,10 @@ class SameConfig:
     stride: int = 16
     transformer_depth: int = 6
     dim_heads: int = 64
+    ff_mult: int = 3
     differential: bool = True
     dyt: bool = True
+    sinusoidal_blocks: int = 0
     sliding_window: tuple[int, int] | None = None
     attention: Literal["xla", "pallas", "hip"] = "xla"
 
@@ -58,6 +60,15 @@ class SameConfig:
         return self.dim // self.dim_heads
 
     @property
+    def ff_inner(self) -> int:
+        return self.dim * self.ff_mult
+
+    def sinusoidal(self, index: int) -> bool:
+        """Block `index` gates its GLU with sin(pi x) instead of SiLU: `sinusoidal_blocks` counts from the end
+        (sa3jax/same_l.py:172-179)."""
+        return index >= self.transformer_depth - self.sinusoidal_blocks + 1
+
+    @property
     def sub_chunk_size(self) -> int:
         """One latent plus `stride` new-token positions: the band half-width w (sa3jax/config.py:129-132)."""
         return self.stride + 1
@@ -65,4 +76,5 @@ class SameConfig:
 
 # The `medium` preset's attention geometry (sa3jax/config.py:171-185) with the MI355X kernels selected.
 MEDIUM_DIT = DiTConfig(embed_dim=1536, num_heads=24, differential=True, attention="hip")
-MEDIUM_SAME_L = SameConfig(channels=256, transformer_depth=12, sliding_window=(1, 1), attention="hip")
+MEDIUM_SAME_L = SameConfig(channels=256, transformer_depth=12, sliding_window=(1, 1), sinusoidal_blocks=8,
+                           attention="hip")

@@ -1,0 +1,187 @@
+// The two elementwise steps of a SAME-L decoder block around the band attention, for gfx950 (MI355X).
+//
+// Replaces the XLA chain of same_l._block (sa3jax/same_l.py:186-192) between its GEMMs:
+//   dyt   out = cast(gamma * tanh(alpha * x) + beta), the fp32 island of same_l._dyt (same_l.py:58-69) cast back
+//         to the compute dtype before the next GEMM, as the block does (same_l.py:191-192);
+//   glu   out = value * act(gate) for the glu_proj output [value | gate] (same_l._feed_forward, same_l.py:172-183),
+//         act = SiLU, or sin(pi * gate) on the sinusoidal blocks.
+// Both are single HBM passes: every thread moves 16-byte chunks (8 bf16 or 4 fp32 elements) of one row, the
+// per-channel parameters come from L1/L2. Cast points are the reference's: bf16 runs round where the XLA chain
+// holds a bf16 array (after the DyT; pi itself, pi * gate and the sine; the sigmoid and the SiLU; the product);
+// fp32 runs do not round.
+#include "api.h"
+#include "common.h"
+
+namespace hb {
+namespace ew {
+
+template <typename T>
+struct Vec;
+template <>
+struct Vec<uint16_t> {  // bf16: 8 elements per 16 bytes
+  static constexpr int N = 8;
+  __device__ static void load(const uint16_t* p, float (&x)[8]) { unpack8(ld16(p), x); }
+  __device__ static void store(uint16_t* p, const float (&x)[8]) { st16(p, pack8(x)); }
+  __device__ static float round(float x) { return round_bf16(x); }
+};
+template <>
+struct Vec<float> {  // fp32: 4 elements per 16 bytes
+  static constexpr int N = 4;
+  __device__ static void load(const float* p, float (&x)[4]) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    for (int i = 0; i < 4; ++i) x[i] = v[i];
+  }
+  __device__ static void store(float* p, const float (&x)[4]) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+  }
+  __device__ static float round(float x) { return x; }
+};
+
+// Both kernels walk the (row, 16-byte chunk) pairs of the tensor with a grid stride, consecutive threads taking
+// consecutive chunks of a row, so every wave moves whole 1 KB runs whatever the row length.
+template <typename T>
+__global__ __launch_bounds__(256) void dyt_kernel(const T* __restrict__ x, int64_t xs, const float* __restrict__ dyt,
+                                                  T* __restrict__ out, int64_t os, int64_t N, int C) {
+  constexpr int V = Vec<T>::N;
+  const int chunks = C / V;
+  const float a2 = 2.f * kLog2e * dyt[0];
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < N * chunks;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t n = i / chunks;
+    const int c0 = static_cast<int>(i - n * chunks) * V;
+    float v[V];
+    Vec<T>::load(x + n * xs + c0, v);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float g = dyt[1 + c0 + j], b = dyt[1 + C + c0 + j];
+      v[j] = dyt_tanh(v[j], a2, -2.f * g, g + b);
+    }
+    Vec<T>::store(out + n * os + c0, v);  // the store's conversion is the single cast
+  }
+}
+
+// The activation with the XLA chain's intermediate arrays: SiLU(g) = g * sigmoid(g) (jax.nn.silu), the sigmoid
+// held in the compute dtype before the product; sin(pi * g) with pi taken in the compute dtype (a Python float
+// times a bf16 array is a bf16 multiply in JAX) and the product held in it before the sine.
+// `bias` (2F values of the compute dtype, or null): the glu_proj layer's bias, added to the GEMM output in the
+// compute dtype first (same_l._linear: the matmul, then the bias add, each held in the compute dtype).
+template <typename T, bool SINE>
+__global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ proj, int64_t ps,
+                                                  const float* __restrict__ bias, T* __restrict__ out, int64_t os,
+                                                  int64_t N, int F) {
+  constexpr int V = Vec<T>::N;
+  const int chunks = F / V;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < N * chunks;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t n = i / chunks;
+    const int c0 = static_cast<int>(i - n * chunks) * V;
+    float val[V], g[V];
+    Vec<T>::load(proj + n * ps + c0, val);
+    Vec<T>::load(proj + n * ps + F + c0, g);
+    if (bias) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        val[i] = Vec<T>::round(val[i] + bias[c0 + i]);
+        g[i] = Vec<T>::round(g[i] + bias[F + c0 + i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      float act;
+      if constexpr (SINE) {
+        act = sinf(Vec<T>::round(Vec<T>::round(static_cast<float>(M_PI)) * g[i]));
+      } else {
+        act = g[i] * Vec<T>::round(__builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * g[i])));
+      }
+      val[i] = val[i] * Vec<T>::round(act);
+    }
+    Vec<T>::store(out + n * os + c0, val);
+  }
+}
+
+}  // namespace ew
+}  // namespace hb
+
+using namespace hb;
+
+namespace {
+
+int check_rows(const char* what, int dtype, const void* in, int64_t in_stride, const void* out, int64_t out_stride,
+               int64_t N, int C, int64_t in_min) {
+  if (dtype != HB_BF16 && dtype != HB_F32) return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0) or HB_F32 (1)", dtype);
+  if (N < 1 || C < 1 || N > (int64_t(1) << 31)) return fail(HB_ERR_SHAPE, "%s needs 1 <= N <= 2^31 and C >= 1", what);
+  const int vec = dtype == HB_BF16 ? 8 : 4;
+  if (C % vec) return fail(HB_ERR_SHAPE, "%s needs the channel count (%d) to be a multiple of %d", what, C, vec);
+  if (in_stride < in_min || out_stride < C || in_stride % vec || out_stride % vec)
+    return fail(HB_ERR_STRIDE, "%s row strides (%lld, %lld) must be >= (%lld, %d) and multiples of %d", what,
+                static_cast<long long>(in_stride), static_cast<long long>(out_stride),
+                static_cast<long long>(in_min), C, vec);
+  if (!in || !out) return fail(HB_ERR_NULL, "%s input and output must be non-NULL", what);
+  if (reinterpret_cast<uintptr_t>(in) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return fail(HB_ERR_STRIDE, "%s input and output must be 16-byte aligned", what);
+  return HB_OK;
+}
+
+// Enough 256-thread blocks for every chunk, at most 16 per CU (the rest is walked with the grid stride).
+dim3 row_grid(int64_t N, int chunks) {
+  const int64_t need = (N * chunks + 255) / 256, cap = 16 * static_cast<int64_t>(device_cus());
+  return dim3(static_cast<unsigned>(need < cap ? need : cap));
+}
+
+int launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(HB_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return HB_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const float* dyt, void* out,
+           int64_t out_row_stride, int64_t N, int C) {
+  clear_error();
+  int st = check_rows("dyt", dtype, x, x_row_stride, out, out_row_stride, N, C, C);
+  if (st) return st;
+  if (!dyt) return fail(HB_ERR_NULL, "dyt parameters must be non-NULL");
+  const int chunks = C / (dtype == HB_BF16 ? 8 : 4);
+  if (dtype == HB_BF16)
+    hipLaunchKernelGGL(ew::dyt_kernel<uint16_t>, row_grid(N, chunks), dim3(256), 0, stream,
+                       static_cast<const uint16_t*>(x), x_row_stride, dyt, static_cast<uint16_t*>(out), out_row_stride,
+                       N, C);
+  else
+    hipLaunchKernelGGL(ew::dyt_kernel<float>, row_grid(N, chunks), dim3(256), 0, stream, static_cast<const float*>(x),
+                       x_row_stride, dyt, static_cast<float*>(out), out_row_stride, N, C);
+  return launched("dyt");
+}
+
+int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_stride, const float* bias,
+           int sinusoidal, void* out, int64_t out_row_stride, int64_t N, int F) {
+  clear_error();
+  int st = check_rows("glu", dtype, proj, proj_row_stride, out, out_row_stride, N, F, static_cast<int64_t>(2) * F);
+  if (st) return st;
+  const int chunks = F / (dtype == HB_BF16 ? 8 : 4);
+  const dim3 grid = row_grid(N, chunks);
+  if (dtype == HB_BF16) {
+    const uint16_t* p = static_cast<const uint16_t*>(proj);
+    uint16_t* o = static_cast<uint16_t*>(out);
+    if (sinusoidal)
+      hipLaunchKernelGGL((ew::glu_kernel<uint16_t, true>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
+    else
+      hipLaunchKernelGGL((ew::glu_kernel<uint16_t, false>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
+  } else {
+    const float* p = static_cast<const float*>(proj);
+    float* o = static_cast<float*>(out);
+    if (sinusoidal)
+      hipLaunchKernelGGL((ew::glu_kernel<float, true>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
+    else
+      hipLaunchKernelGGL((ew::glu_kernel<float, false>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
+  }
+  return launched("glu");
+}
+
+}  // extern "C"

@@ -1,12 +1,14 @@
-"""The SAME-L attention call site with the `attention="hip"` dispatch (sa3jax/same_l.py:151-169).
+"""The SAME-L decoder block with the `attention="hip"` dispatch: its attention step (sa3jax/same_l.py:151-169),
+its feed-forward (sa3jax/same_l.py:172-183) and the block around them (sa3jax/same_l.py:186-192).
 
-Only the attention step of a decoder block is here: `to_qkv` -> differential band attention -> `to_out`.
+`attention="hip"` runs the band attention, the two DyT norms and the GLU gate as HIP kernels and the projections
+as torch GEMMs (hipBLASLt); `attention="xla"` runs the torch restatement of the reference's chain.
 """
 from __future__ import annotations
 
 import torch
 
-from hummingbird_amd import band_attention, xla_chain
+from hummingbird_amd import band_attention, elementwise, xla_chain
 from hummingbird_amd.config import SameConfig
 
 
@@ -32,3 +34,32 @@ def attention(x: torch.Tensor, block: dict, cfg: SameConfig, lam: torch.Tensor |
         out = xla_chain.band_chain(qkv, attn["q_norm"], attn["k_norm"], block["rope_inv_freq"], cfg.num_heads,
                                    cfg.dim_heads, cfg.sub_chunk_size, lam=lam)
     return out @ attn["to_out"]["weight"].t()
+
+
+def _linear(x: torch.Tensor, layer: dict) -> torch.Tensor:
+    """`x @ W^T (+ b)` in the compute dtype (reference: same_l._linear)."""
+    y = x @ layer["weight"].t()
+    return y if layer.get("bias") is None else y + layer["bias"]
+
+
+def feed_forward(x: torch.Tensor, block: dict, index: int, cfg: SameConfig) -> torch.Tensor:
+    """`glu_proj` -> value * act(gate) -> `proj_out` (reference: same_l._feed_forward, same_l.py:172-183); act is
+    sin(pi x) on the last `sinusoidal_blocks` blocks and SiLU before them."""
+    ff = block["ff"]
+    sine = cfg.sinusoidal(index)
+    if use_hip(cfg, x):  # the bias add runs inside the GLU kernel, with the same roundings
+        gated = elementwise.glu(x @ ff["glu_proj"]["weight"].t(), sine, bias=ff["glu_proj"].get("bias"))
+    else:
+        gated = xla_chain.glu(_linear(x, ff["glu_proj"]), sine)
+    return _linear(gated, ff["proj_out"])
+
+
+def block(x: torch.Tensor, params: dict, index: int, cfg: SameConfig,
+          lam: torch.Tensor | None = None) -> torch.Tensor:
+    """One decoder block (reference: same_l._block, same_l.py:186-192):
+    `h = x + attention(DyT(x; pre_norm))`, then `h + feed_forward(DyT(h; ff_norm))`, each DyT in fp32 and cast
+    back to `x.dtype` before its GEMM. `params` holds `pre_norm`, `ff_norm` (DyT params), `self_attn`,
+    `rope_inv_freq` (as `attention` reads them) and `ff.{glu_proj,proj_out}.{weight,bias}`."""
+    norm = elementwise.dyt if use_hip(cfg, x) else xla_chain.dyt_cast
+    h = x + attention(norm(x, params["pre_norm"]), params, cfg, lam=lam)
+    return h + feed_forward(norm(h, params["ff_norm"]), params, index, cfg)

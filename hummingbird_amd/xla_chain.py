@@ -149,3 +149,20 @@ def band_chain(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torch.Te
 
     diff = band(q, k, v32) - lam_v[None, :, None, None] * band(qd, kd, v32)
     return merge(diff.to(dtype))
+
+
+def dyt_cast(x: torch.Tensor, norm: dict) -> torch.Tensor:
+    """DyT in fp32 cast back to `x.dtype` (sa3jax/same_l.py:58-69, 191-192)."""
+    return dyt(x, norm["alpha"], norm["gamma"], norm["beta"]).to(x.dtype)
+
+
+def glu(proj: torch.Tensor, sinusoidal: bool) -> torch.Tensor:
+    """`value * act(gate)` for the glu_proj output `[value | gate]` (sa3jax/same_l.py:172-183) with the XLA chain's
+    intermediate arrays in the compute dtype: SiLU as gate * sigmoid(gate) (jax.nn.silu), sin(pi * gate) with pi
+    itself in the compute dtype (a Python float times an array takes the array's dtype in JAX)."""
+    value, gate = proj.chunk(2, dim=-1)
+    if sinusoidal:
+        act = torch.sin(torch.tensor(math.pi, dtype=proj.dtype, device=proj.device) * gate)
+    else:
+        act = gate * torch.sigmoid(gate)
+    return value * act

@@ -1,7 +1,7 @@
 /* hummingbird_amd: MI355X (gfx950) differential-attention kernels behind a plain C ABI.
  *
- * Two operations replace the reference's two fused TPU kernels (kelechi-c/hummingbird, sa3jax/), and a third
- * the DiT cross-attention chain next to them:
+ * Two operations replace the reference's two fused TPU kernels (kelechi-c/hummingbird, sa3jax/); the others
+ * replace XLA chains next to them (the DiT cross-attention, the SAME-L block's elementwise steps):
  *
  *   hb_dense_diffattn  replaces  dense_attention.dense_attention  (sa3jax/dense_attention.py:104-153),
  *                      called from dit._self_attention (sa3jax/dit.py:191-195);
@@ -9,6 +9,8 @@
  *                      called from same_l._attention (sa3jax/same_l.py:158-161);
  *   hb_cross_prep +    replace   the XLA chain of dit._cross_attention and its hoisted context K/V
  *   hb_cross_attend              (sa3jax/dit.py:203-215, 274-284), which the reference runs without a kernel;
+ *   hb_dyt, hb_glu     replace   the elementwise steps of same_l._block around its GEMMs (sa3jax/same_l.py:58-69,
+ *                                172-192), an XLA chain in the reference;
  *   hb_rope_tables     replaces  band_attention.rope_tables / dit._rope_tables
  *                      (sa3jax/band_attention.py:43-58, sa3jax/dit.py:82-87) in a kernel-native layout.
  *
@@ -149,6 +151,24 @@ int hb_cross_prep(hipStream_t stream, const void* kv, int dtype, int64_t row_str
 int hb_cross_attend(hipStream_t stream, const void* q, int dtype, int64_t row_stride, const float* q_weight,
                     const float* k_weight, const float* lam, void* out, int B, int L, int Nk, int H, int D, float eps,
                     const void* workspace, size_t workspace_bytes);
+
+/* ---- SAME-L decoder block: the elementwise steps around the GEMMs ---------------------------------------
+ * Replace the XLA chain of same_l._block between its GEMMs (sa3jax/same_l.py:186-192).
+ *   hb_dyt : out[n, c] = cast(gamma[c] * tanh(alpha * x[n, c]) + beta[c]), computed in fp32 as same_l._dyt
+ *            (sa3jax/same_l.py:58-69) and cast back to `dtype` before the next GEMM (sa3jax/same_l.py:191-192);
+ *            `dyt` = [alpha, gamma[0..C), beta[0..C)].
+ *   hb_glu : out[n, f] = value * act(gate) with [value | gate] = [proj[n, 0:F] | proj[n, F:2F]]
+ *            (same_l._feed_forward, sa3jax/same_l.py:172-183); act = SiLU(gate) = gate * sigmoid(gate), or
+ *            sin(pi * gate) when `sinusoidal` != 0. For bf16 the intermediate arrays of the XLA chain are rounded
+ *            to bf16 where it holds them (the sigmoid and the SiLU; pi, pi * gate and the sine). `bias` (2F floats
+ *            holding values of the compute dtype, or NULL) is the glu_proj layer's bias: proj holds the bare matmul
+ *            and the bias is added first, rounded to the compute dtype as same_l._linear holds it.
+ *   x, proj, out : N rows with row strides in elements (multiples of 8 for bf16, 4 for fp32), 16-byte aligned;
+ *                  C and F multiples of 8 (bf16) or 4 (fp32);  dtype: HB_BF16 or HB_F32 (input and output). */
+int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const float* dyt, void* out,
+           int64_t out_row_stride, int64_t N, int C);
+int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_stride, const float* bias,
+           int sinusoidal, void* out, int64_t out_row_stride, int64_t N, int F);
 
 #ifdef __cplusplus
 }

@@ -10,6 +10,8 @@ This package restates, in NumPy, the arithmetic of the reference's XLA attention
   (sa3jax/same_l.py:58-69, 84-169), plus the fused-kernel cast profile (sa3jax/band_attention.py:43-120).
 * `oracle.cross` -- DiT cross-attention: q/q_diff RMSNorm, the context's k/k_diff RMSNorm, two softmax
   attentions over the context, subtract (sa3jax/dit.py:203-215, 274-284, 131-176), built from `oracle.dense`.
+* `oracle.block` -- the SAME-L decoder block (sa3jax/same_l.py:58-69, 151-192): DyT, to_qkv, band attention,
+  to_out, residual; DyT, glu_proj, the GLU gate, proj_out, residual; built from `oracle.band`.
 * `oracle.bf16` -- round-to-nearest-even bfloat16 emulation for the cast points.
 
 Only `tests/`, `__graft_entry__.smoke()` and `bench.py`'s CPU-baseline leg may import this package,
@@ -34,10 +36,13 @@ How each function is pinned (the checks live in tests/test_oracle.py):
   index); bit-identical to the dense chain without RoPE and mask when the context has as many tokens as there
   are queries; one context token gives (1 - lambda) v, q = 0 gives (1 - lambda) mean(v); exact cancellation of
   identical branches and linearity in lambda.
+* SAME-L block (tests/test_block.py): the GLU against torch's SiLU and sine in float64; its bf16 cast points on
+  a known case; the block with both branches off is the identity; the FF branch alone against a torch float64
+  composition; the attention branch alone against torch's SDPA under an explicit band mask.
 
 Parity unpinned: the bit-level behaviour of XLA itself (where it rounds einsum outputs, its exp/cos/sin/tanh
 ulps and reduction order) cannot be pinned here because jax is not installed; the oracle fixes the cast
 points the reference's source states, and the tolerance contract (bf16: max-abs <= 2e-2 and cosine >=
 0.9999; fp32: <= 1e-5 relative) absorbs the remaining ulp-level differences.
 """
-from oracle import band, bf16, cross, dense  # noqa: F401
+from oracle import band, bf16, block, cross, dense  # noqa: F401

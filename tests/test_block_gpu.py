@@ -1,0 +1,145 @@
+"""GPU parity of the SAME-L block's elementwise kernels (hb_dyt, hb_glu) and of the block mirror with
+`attention="hip"`.
+
+hb_dyt and hb_glu run against the oracle: fp32 within 1e-5 relative; bf16 within one bf16 step of the oracle's
+value on every element (the kernels' tanh, exp and sine are not bit-identical to NumPy's, so a value that lands
+next to a rounding boundary may round the other way), plus for the DyT a few fp32 units of its operands' scale
+(where gamma * tanh(alpha x) nearly cancels beta, both evaluations carry that absolute error in a tiny result),
+and equal on all but a small fraction. The block with
+`attention="hip"` runs against `attention="xla"` on the GPU and against the oracle, with the attention contract
+(bf16: max-abs <= 2e-2 and cosine >= 0.9999; fp32: 1e-5 relative) applied to the output divided by its largest
+magnitude: the block's output is the residual stream, which carries the block input (values to about 4.5 here),
+and one bf16 step at that magnitude is 0.03.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from hummingbird_amd import elementwise, same_l
+from hummingbird_amd.config import SameConfig
+from oracle import block as oblock
+from tests.block_util import block_params, rounded, to_torch
+from tests.util import assert_bf16_parity, assert_fp32_parity
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RNG = np.random.default_rng(41)
+
+
+def announce(name: str) -> None:
+    print(f"\n[case] {name}", flush=True)
+
+
+def dev(a, dtype=torch.float32) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV, dtype)
+
+
+def assert_within_one_bf16_step(got: np.ndarray, ref: np.ndarray, what: str, atol: float = 0.0,
+                                max_frac: float = 0.01) -> None:
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    step = np.maximum(np.abs(ref), 1e-30) * 2.0 ** -7 + atol  # the spacing of bf16 values around ref (upper bound)
+    diff = np.abs(got - ref)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    assert (diff <= step).all(), f"{what}: {int((diff > step).sum())} elements more than one bf16 step away"
+    frac = float((diff > 0).mean())
+    assert frac <= max_frac, f"{what}: {frac:.3%} of the elements differ (allowed {max_frac:.1%})"
+
+
+DYT_SHAPES = [(1, 8), (100, 512), (3000, 768), (37, 1536)]
+
+
+@pytest.mark.parametrize("shape", DYT_SHAPES, ids=lambda s: "N%dC%d" % s)
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_dyt_vs_oracle(shape, dtype):
+    n, c = shape
+    announce(f"dyt {dtype} {shape}")
+    x = (RNG.standard_normal((n, c)) * 3).astype(np.float32)
+    norm = {"alpha": np.float32(0.7), "gamma": (1 + 0.3 * RNG.standard_normal(c)).astype(np.float32),
+            "beta": (0.1 * RNG.standard_normal(c)).astype(np.float32)}
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    xt = dev(x, tdt)
+    got = elementwise.dyt(xt, {k: torch.as_tensor(v).to(DEV) for k, v in norm.items()}).float().cpu().numpy()
+    ref = oblock.dyt_cast(xt.float().cpu().numpy(), norm, dtype)
+    if dtype == "fp32":
+        assert_fp32_parity(got, ref, f"dyt {shape}")
+    else:
+        scale = float(np.max(np.abs(norm["gamma"]) + np.abs(norm["beta"])))
+        assert_within_one_bf16_step(got, ref, f"dyt {shape}", atol=scale * 2.0 ** -21)
+
+
+GLU_SHAPES = [(1, 8), (200, 1536), (1000, 4608)]
+
+
+@pytest.mark.parametrize("shape", GLU_SHAPES, ids=lambda s: "N%dF%d" % s)
+@pytest.mark.parametrize("sine", [False, True], ids=["silu", "sine"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_glu_vs_oracle(shape, sine, dtype):
+    n, f = shape
+    announce(f"glu {dtype} sine={sine} {shape}")
+    proj = (RNG.standard_normal((n, 2 * f)) * 2).astype(np.float32)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    pt = dev(proj, tdt)
+    got = elementwise.glu(pt, sine).float().cpu().numpy()
+    ref = oblock.glu(pt.float().cpu().numpy(), sine, dtype)
+    if dtype == "fp32":
+        assert_fp32_parity(got, ref, f"glu {shape}")
+    else:
+        assert_within_one_bf16_step(got, ref, f"glu {shape}")
+
+
+@pytest.mark.parametrize("sine", [False, True], ids=["silu", "sine"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_glu_with_bias_vs_oracle(sine, dtype):
+    """The glu_proj bias added inside the kernel equals the bias added to the matmul output in the compute dtype
+    first (same_l._linear), then the GLU."""
+    announce(f"glu with bias {dtype} sine={sine}")
+    n, f = 300, 1536
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    pt = dev((RNG.standard_normal((n, 2 * f)) * 2).astype(np.float32), tdt)
+    bias = dev(0.5 * RNG.standard_normal(2 * f), tdt)  # a parameter of the compute dtype
+    got = elementwise.glu(pt, sine, bias=bias).float().cpu().numpy()
+    summed = oblock.cast(pt.float().cpu().numpy().astype(np.float64) + bias.float().cpu().numpy(), dtype)
+    ref = oblock.glu(summed, sine, dtype)
+    if dtype == "fp32":
+        assert_fp32_parity(got, ref, "glu with bias")
+    else:
+        assert_within_one_bf16_step(got, ref, "glu with bias")
+
+
+def test_elementwise_padded_rows():
+    """Column slices of wider tensors (row stride > width) give the same values as contiguous inputs."""
+    announce("dyt / glu padded rows")
+    x = dev(RNG.standard_normal((64, 520)), torch.bfloat16)
+    norm = {"alpha": torch.tensor(0.5, device=DEV), "gamma": torch.ones(512, device=DEV),
+            "beta": torch.zeros(512, device=DEV)}
+    assert torch.equal(elementwise.dyt(x[:, :512], norm), elementwise.dyt(x[:, :512].contiguous(), norm))
+    p = dev(RNG.standard_normal((2, 32, 3 * 256)), torch.bfloat16)[..., : 2 * 256]
+    assert torch.equal(elementwise.glu(p, False), elementwise.glu(p.contiguous(), False))
+
+
+CFG = SameConfig(channels=64, c_mults=(2,), stride=16, transformer_depth=4, sinusoidal_blocks=2)
+
+
+@pytest.mark.parametrize("index", [0, 3], ids=["silu_block", "sine_block"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_block_hip_vs_xla_and_oracle(index, dtype):
+    """A decoder block (dim 128 = 2 heads of 64, ff 384, half-width 17) with attention="hip" against "xla" on the
+    GPU and against the oracle."""
+    announce(f"same-l block {dtype} index {index}")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    p = block_params(128, 2, 384, seed=50 + index)
+    x = RNG.standard_normal((1, 900, 128)).astype(np.float32)
+    xt = dev(x, tdt)
+    outs = {}
+    for mode in ("hip", "xla"):
+        cfg = SameConfig(channels=64, c_mults=(2,), stride=16, transformer_depth=4, sinusoidal_blocks=2,
+                         attention=mode)
+        outs[mode] = same_l.block(xt, to_torch(p, DEV, tdt), index, cfg).float().cpu().numpy()
+    check = assert_bf16_parity if dtype == "bf16" else assert_fp32_parity
+    scale = max(1.0, float(np.abs(outs["xla"]).max()))
+    check(outs["hip"] / scale, outs["xla"] / scale, f"block {index} hip vs xla (/{scale:.3g})")
+    ref = oblock.block_xla(xt.float().cpu().numpy(), rounded(p, dtype), 2, 64, CFG.sub_chunk_size,
+                           CFG.sinusoidal(index), None, dtype)
+    check(outs["hip"] / scale, ref / scale, f"block {index} hip vs oracle (/{scale:.3g})")
