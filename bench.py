@@ -34,7 +34,7 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
 # (written by hummingbird_amd.rocprof_summary); reported as roofline.traffic when present.
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_120s_clip.json"
 # Kernels that the two calls launch at these shapes (D = 64; window 128 takes the two-tile ring variant).
-DENSE_KERNEL = "dense_attend_bf16<64>"
+DENSE_KERNEL = "dense_attend_bf16<64,128>"
 BAND_KERNEL = "band_ring_bf16<2>"
 
 

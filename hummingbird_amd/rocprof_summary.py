@@ -27,11 +27,12 @@ COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
 
 def short_name(name: str) -> str:
-    """``void hb::dense_attend_bf16<64>(...)`` -> ``dense_attend_bf16<64>`` (also through nested namespaces:
-    ``hb::band_ring::band_ring_bf16<2>`` -> ``band_ring_bf16<2>``); other kernels keep a short prefix."""
-    m = re.search(r"hb::(?:\w+::)*(\w+)(<\d+>)?", name)
+    """``void hb::dense_attend_bf16<64, 128>(...)`` -> ``dense_attend_bf16<64,128>`` (also through nested
+    namespaces: ``hb::band_ring::band_ring_bf16<2>`` -> ``band_ring_bf16<2>``); other kernels keep a short
+    prefix."""
+    m = re.search(r"hb::(?:\w+::)*(\w+)(<\d+(?:,\s*\d+)*>)?", name)
     if m:
-        return m.group(1) + (m.group(2) or "")
+        return m.group(1) + re.sub(r"\s+", "", m.group(2) or "")
     return name.split("(")[0][:60]
 
 
