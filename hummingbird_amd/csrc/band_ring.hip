@@ -61,10 +61,23 @@ struct Prepped {
   u32x4 a1, a2, b1, b2;
 };
 
+struct Par {
+  float g1[8], b1[8], g2[8], b2[8];
+};
+__device__ __forceinline__ Par load_par(const float* __restrict__ par, int m1, int m2) {
+  Par p;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    p.g1[j] = par[8 * m1 + j];
+    p.b1[j] = par[D + 8 * m1 + j];
+    p.g2[j] = par[8 * m2 + j];
+    p.b2[j] = par[D + 8 * m2 + j];
+  }
+  return p;
+}
 // DyT + RoPE (+ scale) of one task; A and B share the DyT parameters `par` = [-2 gamma (D) | gamma + beta (D)].
 // `rot`: the pair is rotated (otherwise cos 1, sin 0).
-__device__ __forceinline__ void prep_task(const Raw& r, int m1, int m2, bool rot, float a2,
-                                          const float* __restrict__ par, float scale, Prepped& o) {
+__device__ __forceinline__ void prep_task(const Raw& r, bool rot, float a2, const Par& p, float scale, Prepped& o) {
   float cs[8] = {r.c0[0], r.c0[1], r.c0[2], r.c0[3], r.c1[0], r.c1[1], r.c1[2], r.c1[3]};
   float sn[8] = {r.s0[0], r.s0[1], r.s0[2], r.s0[3], r.s1[0], r.s1[1], r.s1[2], r.s1[3]};
 #pragma unroll
@@ -79,8 +92,8 @@ __device__ __forceinline__ void prep_task(const Raw& r, int m1, int m2, bool rot
     unpack8(tsr ? r.b2 : r.a2, x2);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float y1 = dyt_tanh(x1[j], a2, par[8 * m1 + j], par[D + 8 * m1 + j]);
-      const float y2 = dyt_tanh(x2[j], a2, par[8 * m2 + j], par[D + 8 * m2 + j]);
+      const float y1 = dyt_tanh(x1[j], a2, p.g1[j], p.b1[j]);
+      const float y2 = dyt_tanh(x2[j], a2, p.g2[j], p.b2[j]);
       // rotate_half: d < half takes -x[d + half], d >= half takes x[d - half]
       o1[j] = __fmaf_rn(y1, cs[j], -(y2 * sn[j])) * scale;
       o2[j] = __fmaf_rn(y2, cs[j], y1 * sn[j]) * scale;
@@ -180,6 +193,7 @@ __device__ __forceinline__ void soft_pv(const f32x16 (&sc)[2], const uint16_t* _
     else
       probs(rt, [&](int r) { return sc[rt][r]; });
   }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     if (!act[g >> 1]) continue;
@@ -228,7 +242,7 @@ struct Stage {
 // Prep waves (4-7): fill the ring at the start of each run, then prepare step j + 1 during step j from rows
 // loaded during step j - 1. The step loop is unrolled by two over stage buffers A and B, so a buffer is loaded
 // in one step and consumed in the next without being copied (a copy would wait for the loads to land).
-template <int C>
+template <int C, bool ALLROT>
 __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16_t* qbuf, const float* qpar,
                                            const float* kpar, float qa2, float ka2, float qscale) {
   constexpr int RING = 2 * C + 1;
@@ -240,7 +254,8 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
   const int pt = t & 255, prow = pt >> 2, pp = pt & 3;
   int m1, m2;
   pair_groups(pp, h8, m1, m2);
-  const bool prot = pp < h8;
+  const bool prot = ALLROT || pp < h8;
+  const Par kp = load_par(kpar, m1, m2), qp = load_par(qpar, m1, m2);
   const Range rg(a);
 
   for (int64_t f = rg.beg; f < rg.end;) {
@@ -313,11 +328,11 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
 #pragma unroll 1
     for (int i = 0; i < RING; ++i) {
       const Stage st = load_stage(j0 - 2 * C + i);  // key tile j0 - C + i (its query rows are not used)
-      prep_task(st.k, m1, m2, prot, ka2, kpar, 1.f, ko);
+      prep_task(st.k, prot, ka2, kp, 1.f, ko);
       store_tile(j0 - C + i, ko, st.v);
       if (i == RING - 1) {
         const Stage sq = load_stage(j0);
-        prep_task(sq.q, m1, m2, prot, qa2, qpar, qscale, qo);
+        prep_task(sq.q, prot, qa2, qp, qscale, qo);
         store_q(qo);
       }
     }
@@ -328,8 +343,8 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
     // One step: prepare step jj + 1 from `cur`, load step jj + 2 into `nxt`, then store after the first barrier.
     auto step = [&](int jj, const Stage& cur, Stage& nxt) {
       const bool next = jj + 1 < j1;
-      prep_task(cur.k, m1, m2, prot, ka2, kpar, 1.f, ko);
-      prep_task(cur.q, m1, m2, prot, qa2, qpar, qscale, qo);
+      prep_task(cur.k, prot, ka2, kp, 1.f, ko);
+      prep_task(cur.q, prot, qa2, qp, qscale, qo);
       // The prepared values are only consumed by the stores after the barrier; pin their computation here, while
       // the attention waves are still busy, instead of letting the compiler sink it past the barrier.
       asm volatile("" ::"v"(ko.a1), "v"(ko.a2), "v"(ko.b1), "v"(ko.b2), "v"(qo.a1), "v"(qo.a2), "v"(qo.b1),
@@ -383,8 +398,9 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
     const float lamh = a.lam ? a.lam[h] : 1.f;
     __syncthreads();  // ring fill
 
-#pragma unroll 1
-    for (int j = j0; j < j1; ++j) {
+    // One step of 64 queries. MODE 0: any step; MODE 1 + qh: an interior step of query half qh.
+    auto do_step = [&](int j, auto mode) {
+      constexpr int MODE = decltype(mode)::value;
       u32x4 qf[4];
       const uint16_t* qsrc = qbuf + br * TE + 32 * qhalf * D;
 #pragma unroll
@@ -427,23 +443,59 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
         soft_pv<FAST>(sc, tile_ptr(i) + 2 * TE, voff, o, lsum, m, c, act[0], act[1], !full[0], !full[1],
                       qlo - kt0 - 4 * lh, static_cast<unsigned>(qhi - qlo));
       };
-      // The K fragments are read one tile ahead of their MFMAs. The loop is unrolled over the two score and
-      // fragment buffers so that all of them stay in fixed registers.
-      f32x16 sa[2], sb[2];
-      u32x4 ka[2][4], kb[2][4];
-      frags(ilo, ka);
-      if (ilo + 1 <= ihi) frags(ilo + 1, kb);
-      scores(ilo, ka, sa);
+      // Interior steps (w = 64 C, and every key of the ring tiles j - C .. j + C inside [0, S)): the wave reads
+      // all RING tiles, half h = 2 i + rt of them takes part iff qhalf <= h <= 4 C + qhalf, and exactly the first
+      // and the last of those are cut by the band edge. That pattern is known at compile time, so the tile loop
+      // is unrolled with no per-tile scalar work and each half's softmax is the masked or unmasked code only.
+      auto run_interior = [&](auto qh) {
+        constexpr int QH = decltype(qh)::value;
+        auto act = [](int hh) { return hh >= QH && hh <= 4 * C + QH; };
+        auto msk = [](int hh) { return hh == QH || hh == 4 * C + QH; };
+        auto fin = [&](int i, const f32x16 (&sc)[2]) {
+          const int kt0 = KT * (j - C + i);
+          soft_pv<FAST>(sc, tile_ptr(i) + 2 * TE, voff, o, lsum, m, c, act(2 * i), act(2 * i + 1), msk(2 * i),
+                        msk(2 * i + 1), qlo - kt0 - 4 * lh, static_cast<unsigned>(qhi - qlo));
+          // Keep the unrolled tiles apart, as the loop iterations of the general path are: scheduled across
+          // tiles, the loads of later tiles would be hoisted and their registers held for the whole step.
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        u32x4 ka[2][4], kb[2][4];
+        f32x16 sa[2], sb[2];
+        frags(0, ka);
+        if (RING > 1) frags(1, kb);
+        qk(ka, qf, sa, act(0), act(1));
+#pragma unroll
+        for (int i = 0; i < RING; i += 2) {
+          if (i + 2 < RING) frags(i + 2, ka);
+          if (i + 1 < RING) qk(kb, qf, sb, act(2 * i + 2), act(2 * i + 3));
+          fin(i, sa);
+          if (i + 1 >= RING) break;
+          if (i + 3 < RING) frags(i + 3, kb);
+          if (i + 2 < RING) qk(ka, qf, sa, act(2 * i + 4), act(2 * i + 5));
+          fin(i + 1, sb);
+        }
+      };
+      if constexpr (MODE > 0) {
+        run_interior(std::integral_constant<int, MODE - 1>{});
+      } else {
+        // The K fragments are read one tile ahead of their MFMAs. The loop is unrolled over the two score and
+        // fragment buffers so that all of them stay in fixed registers.
+        f32x16 sa[2], sb[2];
+        u32x4 ka[2][4], kb[2][4];
+        frags(ilo, ka);
+        if (ilo + 1 <= ihi) frags(ilo + 1, kb);
+        scores(ilo, ka, sa);
 #pragma unroll 1
-      for (int i = ilo;;) {
-        if (i + 2 <= ihi) frags(i + 2, ka);
-        if (i + 1 <= ihi) scores(i + 1, kb, sb);
-        finish(i, sa);
-        if (++i > ihi) break;
-        if (i + 2 <= ihi) frags(i + 2, kb);
-        if (i + 1 <= ihi) scores(i + 1, ka, sa);
-        finish(i, sb);
-        if (++i > ihi) break;
+        for (int i = ilo;;) {
+          if (i + 2 <= ihi) frags(i + 2, ka);
+          if (i + 1 <= ihi) scores(i + 1, kb, sb);
+          finish(i, sa);
+          if (++i > ihi) break;
+          if (i + 2 <= ihi) frags(i + 2, kb);
+          if (i + 1 <= ihi) scores(i + 1, ka, sa);
+          finish(i, sb);
+          if (++i > ihi) break;
+        }
       }
 
       // out = O1 / l1 - lam * O2 / l2, each product rounded on its own. The two branch waves of a query half
@@ -454,11 +506,13 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
       const float li = br == 1 ? __fmul_rn(lamh, inv) : inv;  // this branch's factor
       f32x4* xs = reinterpret_cast<f32x4*>(xbuf) + qhalf * (2 * 4 * 64);  // [d-tile][register / 4][lane][4]
       const int give = 1 - br;                                           // the d-tile the other wave stores
+      // The d-tiles are picked per element with selects: indexing o by the branch would put it on the stack.
+      auto tile_of = [&](int dt, int r) { return dt == 0 ? o[0][r] : o[1][r]; };
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         f32x4 v;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) v[jj] = __fmul_rn(o[give][4 * g + jj], li);
+        for (int jj = 0; jj < 4; ++jj) v[jj] = __fmul_rn(tile_of(give, 4 * g + jj), li);
         xs[(give * 4 + g) * 64 + lane] = v;
       }
       __syncthreads();
@@ -471,7 +525,7 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
           float v[4];
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            const float mine = __fmul_rn(o[dt][4 * g + jj], li);
+            const float mine = __fmul_rn(tile_of(dt, 4 * g + jj), li);
             v[jj] = br == 0 ? __fsub_rn(mine, other[jj]) : __fsub_rn(other[jj], mine);
           }
           if (q < S) {
@@ -483,7 +537,28 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
         }
       }
       __syncthreads();
+    };
+    // Interior steps [ja, jb): w = 64 C and every key of the ring tiles j - C .. j + C inside [0, S), i.e.
+    // 64 j - w >= 0 and 64 j + 63 + w <= S - 1. Each range is its own loop, so that the unrolled interior code
+    // shares no control flow with the general path.
+    int ja = j0, jb = j0;
+    if (w == KT * C && S - QT - w >= 0) {
+      ja = j0 > C ? j0 : C;
+      jb = (S - QT - w) / QT + 1;
+      if (jb > j1) jb = j1;
+      if (jb < ja) ja = jb = j0;
     }
+#pragma unroll 1
+    for (int j = j0; j < ja; ++j) do_step(j, std::integral_constant<int, 0>{});
+    if (qhalf == 0) {
+#pragma unroll 1
+      for (int j = ja; j < jb; ++j) do_step(j, std::integral_constant<int, 1>{});
+    } else {
+#pragma unroll 1
+      for (int j = ja; j < jb; ++j) do_step(j, std::integral_constant<int, 2>{});
+    }
+#pragma unroll 1
+    for (int j = jb; j < j1; ++j) do_step(j, std::integral_constant<int, 0>{});
     f += j1 - j0;
   }
 }
@@ -506,8 +581,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const SoftmaxPlan plan = softmax_plan(dyt_row_bound<D>(a.q_dyt), dyt_row_bound<D>(a.k_dyt), D);
   const float qa2 = 2.f * kLog2e * a.q_dyt[0], ka2 = 2.f * kLog2e * a.k_dyt[0];
   __syncthreads();
-  if (wave_id() >= 4)
-    prep_waves<C>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
+  if (wave_id() >= 4) {
+    if (a.half == D / 2)
+      prep_waves<C, true>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
+    else
+      prep_waves<C, false>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
+  }
   else if (plan.fast)
     attn_waves<C, true>(a, ring, qbuf, xbuf, plan.c);
   else
