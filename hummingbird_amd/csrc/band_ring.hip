@@ -391,10 +391,12 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) koff[kk] = lr * D + 8 * ((2 * kk + lh) ^ kswz);
   const int grp = lane >> 4, mm = lane & 15;
+  // Accumulator o[0] holds the d-tile this wave writes out (dims 32 br .. 32 br + 31), o[1] the one it hands to
+  // the other branch's wave: the branch-2 waves read the V d-tiles in swapped order.
   int voff[2];
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt) {
-    const int col = 32 * dt + 16 * (grp & 1) + 4 * (mm & 3);
+    const int col = 32 * (dt ^ br) + 16 * (grp & 1) + 4 * (mm & 3);
     voff[dt] = (4 * (grp >> 1) + (mm >> 2)) * D + 8 * ((col >> 3) ^ ((mm >> 2) << 1)) + (col & 7);
   }
   const Range rg(a);
@@ -517,13 +519,11 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
       const float li = br == 1 ? __fmul_rn(lamh, inv) : inv;  // this branch's factor
       f32x4* xs = reinterpret_cast<f32x4*>(xbuf) + qhalf * (2 * 4 * 64);  // [d-tile][register / 4][lane][4]
       const int give = 1 - br;                                           // the d-tile the other wave stores
-      // The d-tiles are picked per element with selects: indexing o by the branch would put it on the stack.
-      auto tile_of = [&](int dt, int r) { return dt == 0 ? o[0][r] : o[1][r]; };
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         f32x4 v;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) v[jj] = __fmul_rn(tile_of(give, 4 * g + jj), li);
+        for (int jj = 0; jj < 4; ++jj) v[jj] = __fmul_rn(o[1][4 * g + jj], li);
         xs[(give * 4 + g) * 64 + lane] = v;
       }
       __syncthreads();
@@ -536,7 +536,7 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
           float v[4];
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
-            const float mine = __fmul_rn(tile_of(dt, 4 * g + jj), li);
+            const float mine = __fmul_rn(o[0][4 * g + jj], li);
             v[jj] = br == 0 ? __fsub_rn(mine, other[jj]) : __fsub_rn(other[jj], mine);
           }
           if (q < S) {
