@@ -75,7 +75,7 @@ __device__ __forceinline__ Par load_par(const float* __restrict__ par, int m1, i
   }
   return p;
 }
-// DyT + RoPE (+ scale) of one task; A and B share the DyT parameters `par` = [-2 gamma (D) | gamma + beta (D)].
+// DyT + RoPE (+ scale) of one task; A and B share the DyT parameters `p` (-2 gamma, gamma + beta per dim).
 // `rot`: the pair is rotated (otherwise cos 1, sin 0).
 __device__ __forceinline__ void prep_task(const Raw& r, bool rot, float a2, const Par& p, float scale, Prepped& o) {
   float cs[8] = {r.c0[0], r.c0[1], r.c0[2], r.c0[3], r.c1[0], r.c1[1], r.c1[2], r.c1[3]};
