@@ -89,7 +89,13 @@ __global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ proj, in
     for (int i = 0; i < V; ++i) {
       float act;
       if constexpr (SINE) {
-        act = sinf(Vec<T>::round(Vec<T>::round(static_cast<float>(M_PI)) * g[i]));
+        const float t = Vec<T>::round(Vec<T>::round(static_cast<float>(M_PI)) * g[i]);
+        if constexpr (Vec<T>::N == 8) {
+          // bf16: the hardware sine (v_sin_f32 takes revolutions) is far inside the bf16 rounding of its result
+          act = __builtin_amdgcn_sinf(t * static_cast<float>(0.5 / M_PI));
+        } else {
+          act = sinf(t);
+        }
       } else {
         act = g[i] * Vec<T>::round(__builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * g[i])));
       }
