@@ -91,8 +91,17 @@ __global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ proj, in
       if constexpr (SINE) {
         const float t = Vec<T>::round(Vec<T>::round(static_cast<float>(M_PI)) * g[i]);
         if constexpr (Vec<T>::N == 8) {
-          // bf16: the hardware sine (v_sin_f32 takes revolutions) is far inside the bf16 rounding of its result
-          act = __builtin_amdgcn_sinf(t * static_cast<float>(0.5 / M_PI));
+          // bf16: Cody-Waite reduction of t by 2 pi = C1 + C2 (C1 = 6.28125 has 8 significant bits, so k * C1 is
+          // exact for |k| < 2^16), then the hardware sine (v_sin_f32, argument in revolutions) of the remainder,
+          // |rev| <= 1/2. Its error is far inside the bf16 rounding of the result. Larger |t| take the library sine.
+          constexpr float inv2pi = static_cast<float>(0.5 / M_PI);
+          if (__builtin_expect(fabsf(t) > 65536.f, 0)) {
+            act = sinf(t);
+          } else {
+            const float k = rintf(t * inv2pi);
+            const float r = __fmaf_rn(-k, 1.9353071795864769e-3f, __fmaf_rn(-k, 6.28125f, t));
+            act = __builtin_amdgcn_sinf(r * inv2pi);
+          }
         } else {
           act = sinf(t);
         }

@@ -108,6 +108,18 @@ def test_glu_with_bias_vs_oracle(sine, dtype):
         assert_within_one_bf16_step(got, ref, "glu with bias")
 
 
+@pytest.mark.parametrize("scale", [40.0, 400.0, 30000.0], ids=["gate40", "gate400", "gate30000"])
+def test_glu_sine_large_gates_vs_oracle(scale):
+    """bf16 sine gates far outside the usual range: pi * gate reaches ~500 rad (scale 40) and ~5000 rad (scale
+    400); the kernel reduces the argument by 2 pi before the hardware sine."""
+    announce(f"glu sine large gates x{scale}")
+    proj = (RNG.standard_normal((256, 2 * 512)) * np.r_[np.ones(512), np.full(512, scale)]).astype(np.float32)
+    pt = dev(proj, torch.bfloat16)
+    got = elementwise.glu(pt, True).float().cpu().numpy()
+    ref = oblock.glu(pt.float().cpu().numpy(), True, "bf16")
+    assert_within_one_bf16_step(got, ref, f"glu sine x{scale}", max_frac=0.02)
+
+
 def test_elementwise_padded_rows():
     """Column slices of wider tensors (row stride > width) give the same values as contiguous inputs."""
     announce("dyt / glu padded rows")
