@@ -22,7 +22,12 @@
 //     and its 64 queries (q, q_diff: DyT + RoPE + softmax scale), one (row, RoPE group pair) task each, so the
 //     rotation partner and the cos/sin slice are in the thread's own registers.
 // Two barriers per step: after the first the prep waves store the new tile into the retired slot and the new
-// queries into the query buffer; the second publishes them.
+// queries into the query buffer; the second publishes them. The prep waves run at a higher issue priority.
+//
+// Steps away from the sequence ends with w = 64 C (all but a few per run at w = 128) have a fixed tile pattern:
+// every ring tile is read, and only the first and the last active 32-key half are cut by the band, each by one
+// edge. Those steps run a separate, fully unrolled loop with that pattern built in; the general loop covers the
+// rest.
 //
 // Rows are 128 B without padding; 16-byte chunks are XOR-swizzled per row so that the K fragment reads
 // (ds_read_b128, 8 or 16 rows per cycle), the transposing V reads (ds_read_b64_tr_b16, 4 rows x 32 B per 16
