@@ -17,20 +17,26 @@ from hummingbird_amd.dense_attention import (SUPPORTED_HEAD_DIMS, _f32, _require
 
 __all__ = ["band_attention", "rope_tables", "pack_dyt"]
 
-# RoPE tables keyed by the identity and version of the inv_freq tensor (in-place edits bump the version), so a
-# decoder's repeated calls with the same buffer reuse one table instead of rebuilding it per call.
+# RoPE tables keyed by the identity of the caller's inv_freq tensor, the length and the device, and checked against
+# the tensor's version (in-place edits bump it), so a decoder's repeated calls with the same buffer reuse one table
+# instead of rebuilding it per call. An entry is dropped when its tensor is garbage-collected (weakref.finalize), so
+# callers that build a fresh inv_freq per call do not pile up tables.
 _TABLE_CACHE: dict = {}
+_TABLE_CACHE_MAX = 64
 
 
-def _cached_tables(inv_freq: torch.Tensor, length: int) -> tuple[torch.Tensor, torch.Tensor]:
-    key = (id(inv_freq), inv_freq._version, length, inv_freq.device)
+def _cached_tables(inv_freq: torch.Tensor, length: int, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    key = (id(inv_freq), length, device)
     hit = _TABLE_CACHE.get(key)
-    if hit is not None and hit[0]() is inv_freq:
-        return hit[1], hit[2]
-    cos, sin = rope_tables(length, inv_freq)
-    if len(_TABLE_CACHE) > 64:
-        _TABLE_CACHE.clear()
-    _TABLE_CACHE[key] = (weakref.ref(inv_freq), cos, sin)
+    alive = hit is not None and hit[0]() is inv_freq
+    if alive and hit[1] == inv_freq._version:
+        return hit[2], hit[3]
+    cos, sin = rope_tables(length, inv_freq.to(device) if inv_freq.device != device else inv_freq)
+    if not alive:  # first entry for this tensor: drop it when the tensor dies
+        if len(_TABLE_CACHE) >= _TABLE_CACHE_MAX:
+            _TABLE_CACHE.clear()
+        weakref.finalize(inv_freq, _TABLE_CACHE.pop, key, None)
+    _TABLE_CACHE[key] = (weakref.ref(inv_freq), inv_freq._version, cos, sin)
     return cos, sin
 
 
@@ -82,7 +88,7 @@ def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torc
     cos_p = sin_p = 0
     if half > 0:
         if tables is None:
-            cos, sin = _cached_tables(inv_freq.to(dev) if inv_freq.device != dev else inv_freq, length)
+            cos, sin = _cached_tables(inv_freq, length, dev)
         else:
             cos, sin = (_f32(t, dev) for t in tables)
             if tuple(cos.shape) != (length, half) or tuple(sin.shape) != (length, half):

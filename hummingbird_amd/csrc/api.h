@@ -51,7 +51,7 @@ int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, int s
 int launch_dense_attend_f32(hipStream_t stream, const void* qkv, int64_t rs, int sqd, const float* qw,
                             const float* cosT, const float* sinT, int half, float eps, const void* ws, const float* lam,
                             void* out, int B, int L, int Lk, int H, int D, const DenseLayout& lay);
-// Streaming band kernel (band_ring.hip): bf16, D = 64, half % 16 == 0, window <= 128. Arguments are validated by
+// Streaming band kernel (band_ring.hip): bf16, D = 64, half % 8 == 0, window <= 128. Arguments are validated by
 // hb_band_diffattn before the launch.
 bool band_ring_supported(int dtype, int D, int half, int window);
 int launch_band_ring(hipStream_t stream, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,

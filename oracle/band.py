@@ -129,34 +129,37 @@ def band_grouped_sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, window: int) 
     return np.einsum("gqw,gwd->gqd", w.astype(np.float64), vw).astype(F32).reshape(s, d)
 
 
+def fused_band_attend(qq: np.ndarray, kk: np.ndarray, vv: np.ndarray, window: int, block: int = 512) -> np.ndarray:
+    """One branch of the fused kernel's `attend` (band_attention.py:96-101) for one head of bf16 `qq` (scaled
+    queries), `kk` and `vv`, all `(S, D)`: fp32 logits, -1e30 outside `|k - q| <= window` (and `0 <= k < S`),
+    `w = exp(l - max)` in fp32, `bf16(w) @ V` accumulated in fp32 over the fp32 row sum of the unrounded `w`."""
+    s = qq.shape[0]
+    res = np.empty(qq.shape, F32)
+    for q0 in range(0, s, block):
+        q1 = min(s, q0 + block)
+        k0, k1 = max(0, q0 - window), min(s, q1 + window)
+        logits = (qq[q0:q1].astype(np.float64) @ kk[k0:k1].astype(np.float64).T).astype(F32)
+        band = np.abs(np.arange(k0, k1)[None, :] - np.arange(q0, q1)[:, None]) <= window
+        logits = np.where(band, logits, F32(-1e30))
+        e = np.exp(logits - logits.max(-1, keepdims=True)).astype(F32)
+        res[q0:q1] = ((cast(e, "bf16").astype(np.float64) @ vv[k0:k1].astype(np.float64))
+                      / e.sum(-1, keepdims=True, dtype=np.float64)).astype(F32)
+    return res
+
+
 def band_fused(qkv: np.ndarray, q_norm: dict, k_norm: dict, inv_freq: np.ndarray, num_heads: int, head_dim: int,
                window: int, lam: np.ndarray | None = None, compute: str = "bf16") -> np.ndarray:
-    """The fused TPU kernel's cast points (band_attention.py:82-120): q*scale and k rounded to bf16 after
-    DyT and RoPE, v bf16, fp32 scores masked with -1e30, `exp(l - max)`, `bf16(P) @ V / sum`, fp32 subtraction,
-    one cast."""
+    """The fused TPU kernel's cast points (band_attention.py:82-120): q*scale and k rounded to bf16 after DyT and
+    RoPE in fp32 (85, 104), v rounded to bf16 (94), fp32 scores masked with -1e30, `exp(l - max)`,
+    `bf16(P) @ V / sum` (`fused_band_attend`), fp32 subtraction cast once to the compute dtype (120)."""
     q, k, v, qd, kd = prepare(qkv, q_norm, k_norm, inv_freq, num_heads, head_dim, compute)
     lam = _lam(lam, num_heads)
     scale = F32(1.0 / math.sqrt(head_dim))
     q, qd = cast(q * scale, "bf16"), cast(qd * scale, "bf16")
     k, kd, v = cast(k, "bf16"), cast(kd, "bf16"), cast(v, "bf16")
-    s = qkv.shape[1]
-
-    def attend(qq, kk, vv, block=512):
-        res = np.empty(qq.shape, F32)
-        for q0 in range(0, s, block):
-            q1 = min(s, q0 + block)
-            k0, k1 = max(0, q0 - window), min(s, q1 + window)
-            logits = (qq[q0:q1].astype(np.float64) @ kk[k0:k1].astype(np.float64).T).astype(F32)
-            band = np.abs(np.arange(k0, k1)[None, :] - np.arange(q0, q1)[:, None]) <= window
-            logits = np.where(band, logits, F32(-1e30))
-            e = np.exp(logits - logits.max(-1, keepdims=True)).astype(F32)
-            res[q0:q1] = ((cast(e, "bf16").astype(np.float64) @ vv[k0:k1].astype(np.float64))
-                          / e.sum(-1, keepdims=True, dtype=np.float64)).astype(F32)
-        return res
-
     out = np.empty(q.shape, F32)
     for bi in range(qkv.shape[0]):
         for h in range(num_heads):
-            out[bi, h] = cast(attend(q[bi, h], k[bi, h], v[bi, h]) - lam[h] * attend(qd[bi, h], kd[bi, h], v[bi, h]),
-                              compute)
+            out[bi, h] = cast(fused_band_attend(q[bi, h], k[bi, h], v[bi, h], window)
+                              - lam[h] * fused_band_attend(qd[bi, h], kd[bi, h], v[bi, h], window), compute)
     return merge(out)

@@ -1,7 +1,8 @@
-"""Round-to-nearest-even bfloat16 emulation on float32 arrays (oracle infrastructure).
+"""Round-to-nearest-even bfloat16 and float16 emulation on float32 arrays (oracle infrastructure).
 
-The reference's cast points (`.astype(bf16)`, sa3jax/dtypes.py:23-37 roles) are modelled by
-`round_bf16`, which returns float32 arrays whose values are exactly representable in bfloat16.
+The reference's cast points (`.astype(compute)`, with the compute role bf16, fp16 or fp32 in its presets,
+sa3jax/dtypes.py:23-58) are modelled by `round_bf16` and `round_fp16`, which return float32 arrays whose values
+are exactly representable in the narrower type.
 """
 from __future__ import annotations
 
@@ -21,13 +22,23 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     return out
 
 
+def round_fp16(x: np.ndarray) -> np.ndarray:
+    """float -> nearest IEEE half (ties to even; overflow to inf, gradual underflow), returned as float32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+COMPUTE = ("bf16", "fp16", "fp32")
+
+
 def cast(x: np.ndarray, compute: str) -> np.ndarray:
-    """Cast to the compute dtype ('bf16' or 'fp32'), returned as float32."""
+    """Cast to the compute dtype ('bf16', 'fp16' or 'fp32'), returned as float32."""
     if compute == "bf16":
         return round_bf16(x)
+    if compute == "fp16":
+        return round_fp16(x)
     if compute == "fp32":
         return np.asarray(x, dtype=np.float32)
-    raise ValueError(f"compute must be 'bf16' or 'fp32', got {compute!r}")
+    raise ValueError(f"compute must be one of {COMPUTE}, got {compute!r}")
 
 
 def to_bits(x: np.ndarray) -> np.ndarray:

@@ -12,7 +12,8 @@ Generalisations beyond the reference (each reduces to it at the default): a per-
 second branch (lam = 1 is the reference); `half` follows from `inv_freq.shape[0]` (the reference uses 16 of
 a 64-dim head, config.py:67-70); head_dim 128 is allowed (the XLA chain is general in D, dit.py:113-119).
 
-Arrays are float32 holding values of the compute dtype ('bf16' values are exactly bf16-representable).
+Arrays are float32 holding values of the compute dtype ('bf16' / 'fp16' values are exactly representable in that
+type). The compute dtype follows the reference's presets (sa3jax/dtypes.py:40-58): 'bf16', 'fp16' or 'fp32'.
 """
 from __future__ import annotations
 
@@ -132,29 +133,33 @@ def dense_xla(qkv: np.ndarray, q_weight: np.ndarray, k_weight: np.ndarray, inv_f
     return merge(out)
 
 
+def fused_attend(qq: np.ndarray, kk: np.ndarray, vv: np.ndarray) -> np.ndarray:
+    """One branch of the fused kernel's `attend` (dense_attention.py:79-83) for bf16 `qq` (scaled queries), `kk`
+    and `vv`: fp32 logits, `w = exp(l - max)` in fp32, `bf16(w) @ V` accumulated in fp32, divided by the fp32 row
+    sum of the unrounded `w`."""
+    logits = (qq.astype(np.float64) @ kk.astype(np.float64).T).astype(F32)
+    w = np.exp(logits - logits.max(-1, keepdims=True)).astype(F32)
+    return ((cast(w, "bf16").astype(np.float64) @ vv.astype(np.float64))
+            / w.sum(-1, keepdims=True, dtype=np.float64)).astype(F32)
+
+
 def dense_fused(qkv: np.ndarray, q_weight: np.ndarray, k_weight: np.ndarray, inv_freq: np.ndarray,
                 valid: np.ndarray | None, num_heads: int, head_dim: int, eps: float = 1e-6,
                 lam: np.ndarray | None = None, compute: str = "bf16") -> np.ndarray:
-    """The fused TPU kernel's cast points (dense_attention.py:61-94): K, K_diff, q*scale and masked V rounded
-    to bf16; fp32 scores; `exp(l - max)` unnormalised; `bf16(P) @ V` in fp32 divided by the fp32 row sum;
-    fp32 subtraction and one cast."""
+    """The fused TPU kernel's cast points (dense_attention.py:61-94): RMSNorm and RoPE cast to the compute dtype
+    (62-69), then K, K_diff and masked V rounded to bf16 whatever the compute dtype (75-77), q * scale rounded to
+    bf16 (87-90); fp32 scores, unnormalised exp, `bf16(P) @ V` over the fp32 row sum (`fused_attend`); the fp32
+    subtraction cast once to the compute dtype (94)."""
     q, k, v, qd, kd = prepare(qkv, q_weight, k_weight, inv_freq, valid, num_heads, head_dim, eps, compute)
     lam = _lam(lam, num_heads)
     scale = F32(1.0 / math.sqrt(head_dim))
     k, kd, v = cast(k, "bf16"), cast(kd, "bf16"), cast(v, "bf16")
     q, qd = cast(q * scale, "bf16"), cast(qd * scale, "bf16")
-
-    def attend(qq, kk, vv):
-        logits = (qq.astype(np.float64) @ kk.astype(np.float64).T).astype(F32)
-        w = np.exp(logits - logits.max(-1, keepdims=True)).astype(F32)
-        return ((cast(w, "bf16").astype(np.float64) @ vv.astype(np.float64))
-                / w.sum(-1, keepdims=True, dtype=np.float64)).astype(F32)
-
     out = np.empty(q.shape, F32)
     for bi in range(qkv.shape[0]):
         for h in range(num_heads):
-            out[bi, h] = cast(attend(q[bi, h], k[bi, h], v[bi, h]) - lam[h] * attend(qd[bi, h], kd[bi, h], v[bi, h]),
-                              compute)
+            out[bi, h] = cast(fused_attend(q[bi, h], k[bi, h], v[bi, h])
+                              - lam[h] * fused_attend(qd[bi, h], kd[bi, h], v[bi, h]), compute)
     return merge(out)
 
 

@@ -159,6 +159,15 @@ def test_band_380s_vs_torch_chain():
     got = ba.band_attention(qkv, qn, kn, freq, H, D, w, lam=lam).float().cpu().numpy()
     ref = xla_chain.band_chain(qkv, qn, kn, freq, H, D, w, lam=lam).float().cpu().numpy()
     assert_bf16_parity(got, ref, "380s")
+    # the last head through the oracle (all positions, so RoPE keeps its absolute angles), checked at both ends
+    h = H - 1
+    cols = torch.from_numpy(np.concatenate([np.arange(sec * H * D + h * D, sec * H * D + (h + 1) * D)
+                                            for sec in range(5)])).to(DEV)
+    head_qkv = qkv.index_select(2, cols).float().cpu().numpy()
+    host = lambda n: {k: v.float().cpu().numpy() for k, v in n.items()}  # noqa: E731
+    exp = oband.band_xla(head_qkv, host(qn), host(kn), freq.cpu().numpy(), 1, D, w, lam[h:h + 1].cpu().numpy())[0]
+    for lo, hi in ((0, 300), (S - 300, S)):
+        assert_bf16_parity(got[0, lo:hi, h * D:(h + 1) * D], exp[lo:hi], f"380s last head [{lo},{hi}) vs oracle")
 
 
 RUNS = [  # (B, S, H, window, half, gamma_mean): several 64-query steps per workgroup, runs crossing heads/batches
@@ -183,9 +192,12 @@ def check_vs_torch_chain(b, s, h, d, w, half, gm, label):
     hh = h - 1
     cols = np.concatenate([np.arange(sec * h * d + hh * d, sec * h * d + hh * d + d) for sec in range(5)])
     head = dict(inp, qkv=np.ascontiguousarray(inp["qkv"][-1:, :, cols]), heads=1, lam=inp["lam"][hh:hh + 1])
-    exp = oracle(head, "xla" if gm == 1.0 else "fused")[0]
-    for lo, hi in ((0, 300), (s - 300, s)):
-        assert_bf16_parity(got[-1, lo:hi, hh * d:(hh + 1) * d], exp[lo:hi], f"{label} [{lo},{hi}) vs oracle")
+    if gm == 1.0:
+        exp = oracle(head, "xla")[0]
+        for lo, hi in ((0, 300), (s - 300, s)):
+            assert_bf16_parity(got[-1, lo:hi, hh * d:(hh + 1) * d], exp[lo:hi], f"{label} [{lo},{hi}) vs oracle")
+    else:  # the whole head against the fused-kernel cast points under the bf16 contract
+        assert_bf16_parity(got[-1, :, hh * d:(hh + 1) * d], oracle(head, "fused")[0], f"{label} head vs fused oracle")
 
 
 @pytest.mark.parametrize("shape", RUNS, ids=lambda s: "B%dS%dH%dw%dh%dg%g" % s)
