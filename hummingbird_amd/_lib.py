@@ -31,6 +31,9 @@ SIGNATURES = {
     "hb_dense_diffattn": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                   c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p,
                                   c_size_t]),
+    "hb_dense_noalloc_max_bytes": (c_size_t, []),
+    "hb_dense_diffattn_noalloc": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                                          c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float]),
     "hb_dense_prep": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                               c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t]),
     "hb_dense_attend": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,

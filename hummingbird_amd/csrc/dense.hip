@@ -19,6 +19,8 @@
 // max subtraction, which removes a compare and a subtract per score. Larger gains take the classic online
 // softmax (running max with rescaling) with the reference fused kernel's cast points; the choice is uniform
 // for the whole launch (SoftmaxPlan in attn_tile.h).
+#include <mutex>
+
 #include "api.h"
 #include "attn_tile.h"
 #include "common.h"
@@ -541,4 +543,64 @@ extern "C" int hb_dense_diffattn(hipStream_t stream, const void* qkv, int dtype,
   if (st) return st;
   return hb_dense_attend(stream, qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, lam, out, B, L, H, D, eps,
                          workspace, workspace_bytes);
+}
+
+// ---- The no-allocation entry point ------------------------------------------------------------------------------
+// hb_dense_diffattn_noalloc runs the same two kernels as hb_dense_diffattn with their workspace in `scratch`, a
+// file-scope device array of kNoAllocScratchBytes that every GPU the library runs on holds until the process ends.
+// Host code never passes the array's name to a kernel (on the host it is only a stand-in for the symbol): the
+// device address comes from hipGetSymbolAddress, once per device with that device current, and is kept per device.
+// The prep kernel writes every workspace row the attention kernel reads (zeros past L included), so nothing in the
+// array has to start at zero; each call on a GPU overwrites what the last one left there, so calls that overlap on
+// one GPU (different streams, no ordering between them) race on the array.
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;  // holds the 120 s clip's 49.5 MB bf16 workspace
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device; null until the first call there
+std::mutex g_scratch_mutex;
+
+// Device address of `scratch` on the current device, or null (with the error recorded) if it cannot be had.
+void* device_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(HB_ERR_LAUNCH, "no current HIP device (or device index %d >= %d)", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      fail(HB_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" size_t hb_dense_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int hb_dense_diffattn_noalloc(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
+                                         const float* q_weight, const float* k_weight, const float* cos,
+                                         const float* sin, int half, const float* vmask, const float* lam, void* out,
+                                         int B, int L, int H, int D, float eps) {
+  int st = hb_dense_validate(dtype, row_stride, B, L, H, D, half, eps);
+  if (st) return st;
+  const size_t need = dense_layout(dtype, B, L, H, D).total_bytes;
+  if (need > kNoAllocScratchBytes)
+    return fail(HB_ERR_WORKSPACE,
+                "this shape needs %zu bytes of workspace, more than the %zu-byte no-allocation scratch; call "
+                "hb_dense_diffattn with a workspace instead", need, kNoAllocScratchBytes);
+  if (!qkv || !q_weight || !k_weight || !out) return fail(HB_ERR_NULL, "qkv, q_weight, k_weight and out must be non-NULL");
+  if (half > 0 && (!cos || !sin)) return fail(HB_ERR_NULL, "cos and sin must be non-NULL when half > 0");
+  void* ws = device_scratch();
+  if (!ws) return HB_ERR_LAUNCH;
+  return hb_dense_diffattn(stream, qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, vmask, lam, out, B, L,
+                           H, D, eps, ws, kNoAllocScratchBytes);
 }

@@ -92,6 +92,19 @@ int hb_dense_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t ro
                       const float* q_weight, const float* k_weight, const float* cos, const float* sin, int half,
                       const float* vmask, const float* lam, void* out, int B, int L, int H, int D, float eps,
                       void* workspace, size_t workspace_bytes);
+/* No-allocation variant of hb_dense_diffattn. It has no counterpart in the reference: it is for callers that
+ * cannot allocate device memory or pass a workspace (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). The workspace is a file-scope device array of hb_dense_noalloc_max_bytes() bytes (64 MiB,
+ * which holds the 120 s clip's bf16 workspace), held by every GPU the library runs on until the process ends; its
+ * device address is looked up once per device. Shapes whose hb_dense_workspace_size exceeds it are rejected with
+ * HB_ERR_WORKSPACE before anything runs. The call allocates nothing and otherwise behaves as hb_dense_diffattn.
+ * All calls on one GPU share that GPU's array: calls that overlap on one GPU (streams with no ordering between
+ * them) race and must not be issued. */
+size_t hb_dense_noalloc_max_bytes(void);
+int hb_dense_diffattn_noalloc(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
+                              const float* q_weight, const float* k_weight, const float* cos, const float* sin,
+                              int half, const float* vmask, const float* lam, void* out, int B, int L, int H, int D,
+                              float eps);
 /* Stage 1: RMSNorm + RoPE of k and k_diff and V-masking into `workspace` (kernel-native layout). q_weight is
  * checked but not read. */
 int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,

@@ -132,3 +132,16 @@ def test_workspace_and_alignment_errors_before_any_launch(lib):
     band = lambda ws, wsb: lib.hb_band_diffattn(None, qkv, 0, 5 * H * D, w, w, tab, tab, 32, 200, None, 0x50000,  # noqa: E731
                                                 B, L, H, D, ws, wsb)
     assert band(None, 0) == 8 and band(ws, need - 1) == 8 and band(ws + 64, need) == 8
+
+
+def test_noalloc_rejects_before_touching_the_gpu(lib):
+    """hb_dense_diffattn_noalloc checks the shape and the size of its workspace against its fixed device array
+    before it looks the array up or reads a pointer."""
+    assert lib.hb_dense_noalloc_max_bytes() == 64 << 20
+    fake = 0x100000  # never dereferenced: every call below fails on the host first
+    call = lambda L, D=64, qkv=fake: lib.hb_dense_diffattn_noalloc(  # noqa: E731
+        None, qkv, 0, 5 * 24 * D, fake, fake, fake, fake, 32, None, None, fake, 2, L, 24, D, 1e-6)
+    assert call(6000) == 8       # HB_ERR_WORKSPACE: 3 * 2 * 24 * 6016 * 64 * 2 B > 64 MiB
+    assert b"no-allocation" in lib.hb_last_error()
+    assert call(100, D=96) == 4  # HB_ERR_HEAD_DIM
+    assert call(100, qkv=None) == 1  # HB_ERR_NULL
