@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libhummingbird_amd.so"
 HB_OK = 0
 HB_BF16 = 0
 HB_F32 = 1
+HB_F16 = 2
 
 # status code -> Python exception type. Shape/argument errors mirror the reference's trace-time ValueErrors
 # (sa3jax/dense_attention.py:119-120, sa3jax/band_attention.py:138-140); launch failures are RuntimeErrors.

@@ -49,7 +49,8 @@ int device_cus() {
 }
 
 int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int half) {
-  if (dtype != HB_BF16 && dtype != HB_F32) return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0) or HB_F32 (1)", dtype);
+  if (dtype != HB_BF16 && dtype != HB_F32 && dtype != HB_F16)
+    return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0), HB_F32 (1) or HB_F16 (2)", dtype);
   if (D != 64 && D != 128) return fail(HB_ERR_HEAD_DIM, "head_dim %d is not 64 or 128", D);
   if (B < 1 || N < 1 || H < 1) return fail(HB_ERR_SHAPE, "need B, N, H >= 1 (B=%d, N=%d, H=%d)", B, N, H);
   if (B > 65535 || H > 65535 || N > (1 << 28))
@@ -89,7 +90,8 @@ const char* hb_status_name(int status) {
 }
 
 size_t hb_dense_workspace_size(int dtype, int B, int L, int H, int D) {
-  if ((dtype != HB_BF16 && dtype != HB_F32) || B < 1 || L < 1 || H < 1 || (D != 64 && D != 128)) return 0;
+  if ((dtype != HB_BF16 && dtype != HB_F32 && dtype != HB_F16) || B < 1 || L < 1 || H < 1 || (D != 64 && D != 128))
+    return 0;
   return hb::dense_layout(dtype, B, L, H, D).total_bytes;
 }
 

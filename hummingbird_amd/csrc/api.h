@@ -35,32 +35,34 @@ int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int 
 // Multiprocessor (CU) count of the current device, queried once per device (256 if the query fails).
 int device_cus();
 
-// Dense kernels (dense.hip: bf16, fp32.hip: fp32). Arguments are validated by the exported entry points before
+// Dense kernels (dense.hip: bf16 and half, fp32.hip: fp32). Arguments are validated by the exported entry points before
 // these are called. The prep reads k, k_diff and v from sections sk, skd and sv of the rows of `kv` (units of
 // H * D elements) for Lk keys into the workspace described by `lay` (laid out for Lk keys); the attention reads
 // q and q_diff from sections 0 and sqd of the rows of `q` for L queries and attends over the Lk prepared keys.
-int launch_dense_prep_bf16(hipStream_t stream, const void* kv, int64_t rs, int sk, int skd, int sv, const float* kw,
-                           const float* cos, const float* sin, int half, const float* vmask, int B, int Lk, int H,
-                           int D, float eps, const DenseLayout& lay, void* workspace);
-int launch_dense_attend_bf16(hipStream_t stream, const void* q, int64_t rs, int sqd, const float* qw, const float* kw,
-                             const float* cos, const float* sin, int half, float eps, const float* lam, void* out,
-                             int B, int L, int Lk, int H, int D, const DenseLayout& lay, const void* workspace);
+// 16-bit inputs (dtype HB_BF16 or HB_F16: bf16 or half qkv and out; the operands are bf16 in both).
+int launch_dense_prep_16bit(hipStream_t stream, int dtype, const void* kv, int64_t rs, int sk, int skd, int sv,
+                            const float* kw, const float* cos, const float* sin, int half, const float* vmask, int B,
+                            int Lk, int H, int D, float eps, const DenseLayout& lay, void* workspace);
+int launch_dense_attend_16bit(hipStream_t stream, int dtype, const void* q, int64_t rs, int sqd, const float* qw,
+                              const float* kw, const float* cos, const float* sin, int half, float eps,
+                              const float* lam, void* out, int B, int L, int Lk, int H, int D, const DenseLayout& lay,
+                              const void* workspace);
 int launch_dense_prep_f32(hipStream_t stream, const void* qkv, int64_t rs, int sk, int skd, int sv, const float* kw,
                           const float* cosT, const float* sinT, int half, const float* vmask, int B, int L, int H, int D,
                           float eps, const DenseLayout& lay, void* ws);
 int launch_dense_attend_f32(hipStream_t stream, const void* qkv, int64_t rs, int sqd, const float* qw,
                             const float* cosT, const float* sinT, int half, float eps, const void* ws, const float* lam,
                             void* out, int B, int L, int Lk, int H, int D, const DenseLayout& lay);
-// Streaming band kernel (band_ring.hip): bf16, D = 64, half % 8 == 0, window <= 128. Arguments are validated by
-// hb_band_diffattn before the launch.
+// Streaming band kernel (band_ring.hip): bf16 or half, D = 64, half % 8 == 0, window <= 128. Arguments are
+// validated by hb_band_diffattn before the launch.
 bool band_ring_supported(int dtype, int D, int half, int window);
-int launch_band_ring(hipStream_t stream, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
+int launch_band_ring(hipStream_t stream, int dtype, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
                      const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                      int S, int H);
-// Tiled band kernels (band_tiled.hip): bf16, any head_dim and half-width; the workspace holds the prepared keys
-// in the dense layout (three (B, H, round_up(S, 128), D) regions: k', k_diff', v'^T).
+// Tiled band kernels (band_tiled.hip): bf16 or half, any head_dim and half-width; the workspace holds the prepared
+// keys in the dense layout (three (B, H, round_up(S, 128), D) bf16 regions: k', k_diff', v'^T).
 DenseLayout band_tiled_layout(int B, int S, int H, int D);
-int launch_band_tiled(hipStream_t stream, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
+int launch_band_tiled(hipStream_t stream, int dtype, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
                       const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                       int S, int H, int D, void* workspace);
 int launch_band_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qdyt, const float* kdyt,

@@ -164,9 +164,10 @@ __device__ __forceinline__ float inv_rowsum(const float (&lsum)[NB][NCT], int br
   return __frcp_rn(lsum[br][ct] + __shfl_xor(lsum[br][ct], 32, kWave));
 }
 
-// out[q, h*D + d] = O1/l1 - lam * O2/l2 for this lane's query of column tile ct, written as bf16 in groups of
-// 4 dims. Every lane must call it (it combines the two lane halves); `orow` may be null for queries >= N.
-template <int D, int NCT>
+// out[q, h*D + d] = O1/l1 - lam * O2/l2 for this lane's query of column tile ct, written in the output type IO
+// (bf16 or half) in groups of 4 dims. Every lane must call it (it combines the two lane halves); `orow` may be null
+// for queries >= N.
+template <int D, int NCT, class IO = Bf16Io>
 __device__ __forceinline__ void store_diff_bf16(uint16_t* __restrict__ orow, const f32x16 (&o)[2][NCT][D / 32],
                                                 const float (&lsum)[2][NCT], int ct, float lam) {
   const int lh = (threadIdx.x & 63) >> 5;
@@ -181,8 +182,8 @@ __device__ __forceinline__ void store_diff_bf16(uint16_t* __restrict__ orow, con
       for (int j = 0; j < 4; ++j)  // rounded products: identical branches cancel exactly, as in the reference
         v[j] = __fsub_rn(__fmul_rn(o[0][ct][dt][4 * g + j], i0), __fmul_rn(o[1][ct][dt][4 * g + j], i1));
       u32x2 pk;
-      pk[0] = pack_bf16x2(v[0], v[1]);
-      pk[1] = pack_bf16x2(v[2], v[3]);
+      pk[0] = IO::pack2(v[0], v[1]);
+      pk[1] = IO::pack2(v[2], v[3]);
       *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * lh) = pk;
     }
 }

@@ -2,9 +2,9 @@
 //
 // Replaces the reference's fused TPU kernel sa3jax/band_attention.py:123-180 (and the XLA chain
 // sa3jax/same_l.py:151-169):
-//   - bf16, head_dim 64, half-width w <= 128: the streaming ring kernel (band_ring.hip), which keeps the whole
-//     key window of a 64-query step in LDS and prepares every key once per run; no workspace;
-//   - bf16, w > 128 or head_dim 128: the tiled kernels (band_tiled.hip), which prepare the keys into a
+//   - bf16 or half, head_dim 64, half-width w <= 128: the streaming ring kernel (band_ring.hip), which keeps the
+//     whole key window of a 64-query step in LDS and prepares every key once per run; no workspace;
+//   - bf16 or half, w > 128 or head_dim 128: the tiled kernels (band_tiled.hip), which prepare the keys into a
 //     caller-supplied workspace and stream each 128-query block's window through LDS;
 //   - fp32: the fp32 kernel (fp32.hip); no workspace.
 #include "api.h"
@@ -12,11 +12,12 @@
 using namespace hb;
 
 static bool band_needs_workspace(int dtype, int D, int half, int window) {
-  return dtype == HB_BF16 && !band_ring_supported(dtype, D, half, window);
+  return dtype != HB_F32 && !band_ring_supported(dtype, D, half, window);
 }
 
 extern "C" size_t hb_band_workspace_size(int dtype, int B, int S, int H, int D, int half, int window) {
-  if ((dtype != HB_BF16 && dtype != HB_F32) || B < 1 || S < 1 || H < 1 || (D != 64 && D != 128)) return 0;
+  if ((dtype != HB_BF16 && dtype != HB_F32 && dtype != HB_F16) || B < 1 || S < 1 || H < 1 || (D != 64 && D != 128))
+    return 0;
   if (!band_needs_workspace(dtype, D, half, window > S ? S : window)) return 0;
   return band_tiled_layout(B, S, H, D).total_bytes;
 }
@@ -41,11 +42,11 @@ extern "C" int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, 
   }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
   if (band_ring_supported(dtype, D, half, window))
-    return launch_band_ring(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H);
+    return launch_band_ring(stream, dtype, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H);
   const size_t need = band_tiled_layout(B, S, H, D).total_bytes;
   if (!workspace) return fail(HB_ERR_WORKSPACE, "this shape needs a workspace of %zu bytes (hb_band_workspace_size)", need);
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(HB_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (workspace_bytes < need) return fail(HB_ERR_WORKSPACE, "workspace holds %zu bytes, needs %zu", workspace_bytes, need);
-  return launch_band_tiled(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D,
+  return launch_band_tiled(stream, dtype, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D,
                            workspace);
 }

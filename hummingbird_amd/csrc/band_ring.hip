@@ -1,7 +1,8 @@
 // SAME-L sliding-window (band) differential attention, streaming form, for gfx950 (MI355X).
 //
 // Replaces the reference's fused TPU kernel sa3jax/band_attention.py:61-180 and the XLA chain
-// sa3jax/same_l.py:151-169 for head_dim 64, half-width w <= 128, bf16, rotary half-width a multiple of 8.
+// sa3jax/same_l.py:151-169 for head_dim 64, half-width w <= 128, bf16 or half inputs (bf16 operands either way),
+// rotary half-width a multiple of 8.
 //
 // One workgroup of 8 waves per CU walks a contiguous run of 64-query steps along the sequence of one
 // (batch, head). The keys step j can reach, [64j - 64C, 64j + 64 + 64C) with C = ceil(w / 64), live in an LDS
@@ -82,6 +83,7 @@ __device__ __forceinline__ Par load_par(const float* __restrict__ par, int m1, i
 }
 // DyT + RoPE (+ scale) of one task; A and B share the DyT parameters `p` (-2 gamma, gamma + beta per dim).
 // `rot`: the pair is rotated (otherwise cos 1, sin 0).
+template <class IO>
 __device__ __forceinline__ void prep_task(const Raw& r, bool rot, float a2, const Par& p, float scale, Prepped& o) {
   float cs[8] = {r.c0[0], r.c0[1], r.c0[2], r.c0[3], r.c1[0], r.c1[1], r.c1[2], r.c1[3]};
   float sn[8] = {r.s0[0], r.s0[1], r.s0[2], r.s0[3], r.s1[0], r.s1[1], r.s1[2], r.s1[3]};
@@ -93,8 +95,8 @@ __device__ __forceinline__ void prep_task(const Raw& r, bool rot, float a2, cons
 #pragma unroll
   for (int tsr = 0; tsr < 2; ++tsr) {
     float x1[8], x2[8], o1[8], o2[8];
-    unpack8(tsr ? r.b1 : r.a1, x1);
-    unpack8(tsr ? r.b2 : r.a2, x2);
+    IO::unpack8(tsr ? r.b1 : r.a1, x1);
+    IO::unpack8(tsr ? r.b2 : r.a2, x2);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float y1 = dyt_tanh(x1[j], a2, p.g1[j], p.b1[j]);
@@ -255,7 +257,7 @@ struct Stage {
 // Prep waves (4-7): fill the ring at the start of each run, then prepare step j + 1 during step j from rows
 // loaded during step j - 1. The step loop is unrolled by two over stage buffers A and B, so a buffer is loaded
 // in one step and consumed in the next without being copied (a copy would wait for the loads to land).
-template <int C, bool ALLROT>
+template <class IO, int C, bool ALLROT>
 __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16_t* qbuf, const float* qpar,
                                            const float* kpar, float qa2, float ka2, float qscale) {
   constexpr int RING = 2 * C + 1;
@@ -326,7 +328,8 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
       for (int u = 0; u < 2; ++u) {
         const int ch = pt + 256 * u, vpos = KT * kt + (ch >> 3);
         const bool in = vpos >= 0 && vpos < S;
-        *reinterpret_cast<u32x4*>(base + 2 * TE + vofs(ch >> 3, ch & 7)) = in ? v[u] : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(base + 2 * TE + vofs(ch >> 3, ch & 7)) =
+            in ? IO::to_bf16x8(v[u]) : u32x4{0u, 0u, 0u, 0u};
       }
     };
     auto store_q = [&](const Prepped& qo) {
@@ -341,11 +344,11 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
 #pragma unroll 1
     for (int i = 0; i < RING; ++i) {
       const Stage st = load_stage(j0 - 2 * C + i);  // key tile j0 - C + i (its query rows are not used)
-      prep_task(st.k, prot, ka2, kp, 1.f, ko);
+      prep_task<IO>(st.k, prot, ka2, kp, 1.f, ko);
       store_tile(j0 - C + i, ko, st.v);
       if (i == RING - 1) {
         const Stage sq = load_stage(j0);
-        prep_task(sq.q, prot, qa2, qp, qscale, qo);
+        prep_task<IO>(sq.q, prot, qa2, qp, qscale, qo);
         store_q(qo);
       }
     }
@@ -356,8 +359,8 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
     // One step: prepare step jj + 1 from `cur`, load step jj + 2 into `nxt`, then store after the first barrier.
     auto step = [&](int jj, const Stage& cur, Stage& nxt) {
       const bool next = jj + 1 < j1;
-      prep_task(cur.k, prot, ka2, kp, 1.f, ko);
-      prep_task(cur.q, prot, qa2, qp, qscale, qo);
+      prep_task<IO>(cur.k, prot, ka2, kp, 1.f, ko);
+      prep_task<IO>(cur.q, prot, qa2, qp, qscale, qo);
       // The prepared values are only consumed by the stores after the barrier; pin their computation here, while
       // the attention waves are still busy, instead of letting the compiler sink it past the barrier.
       asm volatile("" ::"v"(ko.a1), "v"(ko.a2), "v"(ko.b1), "v"(ko.b2), "v"(qo.a1), "v"(qo.a2), "v"(qo.b1),
@@ -382,7 +385,7 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
 }
 
 // Attention waves (0-3), wave = (query half, branch).
-template <int C, bool FAST>
+template <class IO, int C, bool FAST>
 __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16_t* qbuf, float* xbuf, float c) {
   constexpr int RING = 2 * C + 1;
   const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
@@ -545,8 +548,8 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
           }
           if (q < S) {
             u32x2 pk;
-            pk[0] = pack_bf16x2(v[0], v[1]);
-            pk[1] = pack_bf16x2(v[2], v[3]);
+            pk[0] = IO::pack2(v[0], v[1]);
+            pk[1] = IO::pack2(v[2], v[3]);
             *reinterpret_cast<u32x2*>(orow + 8 * g + 4 * lh) = pk;
           }
         }
@@ -578,8 +581,9 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
   }
 }
 
-template <int C>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void band_ring_bf16(Args a) {
+// IO: the element type of qkv and out (bf16 or half); the operands are bf16 either way.
+template <class IO, int C>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void band_ring(Args a) {
   constexpr int RING = 2 * C + 1;
   __shared__ __attribute__((aligned(16))) uint16_t ring[RING * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t qbuf[2 * TE];  // q, q_diff of the step (64 rows each)
@@ -600,23 +604,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // The prep waves issue first when both roles of a SIMD are ready: measured 6% faster than equal priority.
     __builtin_amdgcn_s_setprio(1);
     if (a.half == D / 2)
-      prep_waves<C, true>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
+      prep_waves<IO, C, true>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
     else
-      prep_waves<C, false>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
+      prep_waves<IO, C, false>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
   }
   else if (plan.fast)
-    attn_waves<C, true>(a, ring, qbuf, xbuf, plan.c);
+    attn_waves<IO, C, true>(a, ring, qbuf, xbuf, plan.c);
   else
-    attn_waves<C, false>(a, ring, qbuf, xbuf, plan.c);
+    attn_waves<IO, C, false>(a, ring, qbuf, xbuf, plan.c);
 }
 
 }  // namespace band_ring
 
 bool band_ring_supported(int dtype, int D, int half, int window) {
-  return dtype == HB_BF16 && D == band_ring::D && half % 8 == 0 && window <= 128;
+  return (dtype == HB_BF16 || dtype == HB_F16) && D == band_ring::D && half % 8 == 0 && window <= 128;
 }
 
-int launch_band_ring(hipStream_t stream, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
+int launch_band_ring(hipStream_t stream, int dtype, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
                      const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                      int S, int H) {
   using namespace band_ring;
@@ -638,12 +642,11 @@ int launch_band_ring(hipStream_t stream, const void* qkv, int64_t rs, const floa
   a.out = static_cast<uint16_t*>(out);
   const int64_t grid = a.total < ncu ? a.total : ncu;
   const int C = (window + 63) / 64;
-  if (C == 0)
-    hipLaunchKernelGGL(band_ring_bf16<0>, dim3(static_cast<unsigned>(grid)), dim3(NT), 0, stream, a);
-  else if (C == 1)
-    hipLaunchKernelGGL(band_ring_bf16<1>, dim3(static_cast<unsigned>(grid)), dim3(NT), 0, stream, a);
-  else
-    hipLaunchKernelGGL(band_ring_bf16<2>, dim3(static_cast<unsigned>(grid)), dim3(NT), 0, stream, a);
+  const bool f16 = dtype == HB_F16;
+  auto kernel = C == 0 ? (f16 ? hb::band_ring::band_ring<F16Io, 0> : hb::band_ring::band_ring<Bf16Io, 0>)
+                : C == 1 ? (f16 ? hb::band_ring::band_ring<F16Io, 1> : hb::band_ring::band_ring<Bf16Io, 1>)
+                         : (f16 ? hb::band_ring::band_ring<F16Io, 2> : hb::band_ring::band_ring<Bf16Io, 2>);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(grid)), dim3(NT), 0, stream, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(HB_ERR_LAUNCH, "band_ring launch failed: %s", hipGetErrorString(e));
   return HB_OK;

@@ -1,5 +1,6 @@
 // SAME-L sliding-window (band) differential attention for the shapes the streaming ring kernel does not take:
-// half-widths w > 128 (whose key window does not fit an LDS ring) and head_dim 128, bf16.
+// half-widths w > 128 (whose key window does not fit an LDS ring) and head_dim 128, bf16 or half inputs (bf16
+// operands either way).
 //
 // Replaces the reference's fused TPU kernel sa3jax/band_attention.py:61-180 and the XLA chain
 // sa3jax/same_l.py:151-169 on those shapes. Two kernels run back to back on the caller's stream, on the dense
@@ -28,11 +29,12 @@ namespace band_tiled {
 // DyT + RoPE of k and k_diff (and V transposed) for 64 keys of one head. Thread task = (key, RoPE group pair) as
 // in the dense prep: the rotation partner and the cos / sin slice are in the thread's own registers.
 // `kdyt` = [alpha, gamma[D], beta[D]]; `half` % 8 == 0 (checked on the host).
-template <int D>
-__global__ __launch_bounds__(256) void band_prep_bf16(const uint16_t* __restrict__ qkv, int64_t rs,
-                                                      const float* __restrict__ kdyt, const float* __restrict__ cosT,
-                                                      const float* __restrict__ sinT, int half, int S, int Sp, int H,
-                                                      int64_t region, uint16_t* __restrict__ ws) {
+// IO: the element type of qkv (bf16 or half); the keys are prepared in bf16 either way.
+template <class IO, int D>
+__global__ __launch_bounds__(256) void band_prep(const uint16_t* __restrict__ qkv, int64_t rs,
+                                                 const float* __restrict__ kdyt, const float* __restrict__ cosT,
+                                                 const float* __restrict__ sinT, int half, int S, int Sp, int H,
+                                                 int64_t region, uint16_t* __restrict__ ws) {
   constexpr int PAIRS = D / 16;
   constexpr int TASKS = 64 * PAIRS / 256;
   constexpr int VCH = 64 * D / 8 / 256;
@@ -91,8 +93,8 @@ __global__ __launch_bounds__(256) void band_prep_bf16(const uint16_t* __restrict
 #pragma unroll
     for (int si = 0; si < 2; ++si) {
       float x1[8], x2[8], o1[8], o2[8];
-      unpack8(raw[i][si][0], x1);
-      unpack8(raw[i][si][1], x2);
+      IO::unpack8(raw[i][si][0], x1);
+      IO::unpack8(raw[i][si][1], x2);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float g1 = kdyt[1 + 8 * m1 + j], b1 = kdyt[1 + D + 8 * m1 + j];
@@ -109,14 +111,14 @@ __global__ __launch_bounds__(256) void band_prep_bf16(const uint16_t* __restrict
     }
   }
 
-  // V, transposed per 64-key tile (v_tile_key order) through LDS, the 16-byte chunks of row r XOR-swizzled by
-  // (r / 8) % 8 so that the column reads are free of bank conflicts.
+  // V (rounded to bf16, band_attention.py:94), transposed per 64-key tile (v_tile_key order) through LDS, the
+  // 16-byte chunks of row r XOR-swizzled by (r / 8) % 8.
   __shared__ __attribute__((aligned(16))) uint16_t vt[64 * D];
   auto vt_at = [](int row, int col) { return row * D + 8 * ((col >> 3) ^ ((row >> 3) & 7)) + (col & 7); };
 #pragma unroll
   for (int i = 0; i < VCH; ++i) {
     const int ch = t + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8;
-    *reinterpret_cast<u32x4*>(vt + vt_at(key, col)) = vraw[i];
+    *reinterpret_cast<u32x4*>(vt + vt_at(key, col)) = IO::to_bf16x8(vraw[i]);
   }
   __syncthreads();
 #pragma unroll
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(256) void band_prep_bf16(const uint16_t* __restrict
 // DyT, rotate-half RoPE over the first 2 * 8 H8 dims and the softmax scale of one query row held whole by this
 // lane, in fp32 with one bf16 rounding (the reference fused kernel's cast points, band_attention.py:82-85, 104).
 // `row`: its D elements in qkv; `cs` / `sn`: its (half) columns of the tables; `qdyt` = [alpha, gamma, beta].
-template <int D, int H8>
+template <class IO, int D, int H8>
 __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, const float* __restrict__ qdyt,
                                            const float* __restrict__ cs, const float* __restrict__ sn, float qscale,
                                            u32x4 (&out)[D / 8]) {
@@ -158,7 +160,7 @@ __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, con
 #pragma unroll
   for (int c = 0; c < D / 8; ++c) {
     float x[8];
-    unpack8(raw[c], x);
+    IO::unpack8(raw[c], x);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int d = 8 * c + j;
@@ -233,8 +235,9 @@ __device__ __forceinline__ void band_tiles(const TileCopy<D>& issue, int S, int 
   }
 }
 
-template <int D>
-__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void band_attend_bf16(
+// IO: the element type of qkv and out (bf16 or half); the operands are bf16 either way.
+template <class IO, int D>
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void band_attend(
     const uint16_t* __restrict__ qkv, int64_t rs, const float* __restrict__ qdyt, const float* __restrict__ kdyt,
     const float* __restrict__ cosT, const float* __restrict__ sinT, int half, int w, const uint16_t* __restrict__ ws,
     int64_t region, int B, int S, int Sp, int H, const float* __restrict__ lam, uint16_t* __restrict__ out) {
@@ -267,20 +270,20 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void band_attend_bf16(
     const float* sn = sinT + static_cast<int64_t>(qc) * half;
     u32x4 whole[D / 8];
     switch (half / 8) {  // half % 8 == 0 and half <= D / 2 are checked on the host
-      case 0: prep_q_row<D, 0>(row, qdyt, cs, sn, plan.qscale, whole); break;
-      case 1: prep_q_row<D, 1>(row, qdyt, cs, sn, plan.qscale, whole); break;
-      case 2: prep_q_row<D, 2>(row, qdyt, cs, sn, plan.qscale, whole); break;
-      case 3: prep_q_row<D, 3>(row, qdyt, cs, sn, plan.qscale, whole); break;
+      case 0: prep_q_row<IO, D, 0>(row, qdyt, cs, sn, plan.qscale, whole); break;
+      case 1: prep_q_row<IO, D, 1>(row, qdyt, cs, sn, plan.qscale, whole); break;
+      case 2: prep_q_row<IO, D, 2>(row, qdyt, cs, sn, plan.qscale, whole); break;
+      case 3: prep_q_row<IO, D, 3>(row, qdyt, cs, sn, plan.qscale, whole); break;
       default:
         if constexpr (D == 64) {
-          prep_q_row<D, 4>(row, qdyt, cs, sn, plan.qscale, whole);
+          prep_q_row<IO, D, 4>(row, qdyt, cs, sn, plan.qscale, whole);
         } else {
           switch (half / 8) {
-            case 4: prep_q_row<D, 4>(row, qdyt, cs, sn, plan.qscale, whole); break;
-            case 5: prep_q_row<D, 5>(row, qdyt, cs, sn, plan.qscale, whole); break;
-            case 6: prep_q_row<D, 6>(row, qdyt, cs, sn, plan.qscale, whole); break;
-            case 7: prep_q_row<D, 7>(row, qdyt, cs, sn, plan.qscale, whole); break;
-            default: prep_q_row<D, 8>(row, qdyt, cs, sn, plan.qscale, whole); break;
+            case 4: prep_q_row<IO, D, 4>(row, qdyt, cs, sn, plan.qscale, whole); break;
+            case 5: prep_q_row<IO, D, 5>(row, qdyt, cs, sn, plan.qscale, whole); break;
+            case 6: prep_q_row<IO, D, 6>(row, qdyt, cs, sn, plan.qscale, whole); break;
+            case 7: prep_q_row<IO, D, 7>(row, qdyt, cs, sn, plan.qscale, whole); break;
+            default: prep_q_row<IO, D, 8>(row, qdyt, cs, sn, plan.qscale, whole); break;
           }
         }
     }
@@ -323,16 +326,16 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void band_attend_bf16(
     band_tiles<D, false>(copy, S, w, t_lo, t_hi, qa, nq, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
 
   static_assert(2 * NCT * (D / 32) * 16 * 64 * 4 <= 2 * T::STAGE * 2, "exchange buffer exceeds the two stages");
-  store_diff_split<D>(out, b, S, H, h, qa, br0, lam ? lam[h] : 1.f, o, lsum, smem);
+  store_diff_split<D, 128, IO>(out, b, S, H, h, qa, br0, lam ? lam[h] : 1.f, o, lsum, smem);
 }
 
 }  // namespace band_tiled
 
 DenseLayout band_tiled_layout(int B, int S, int H, int D) { return dense_layout(HB_BF16, B, S, H, D); }
 
-int launch_band_tiled(hipStream_t stream, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
-                      const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
-                      int S, int H, int D, void* workspace) {
+int launch_band_tiled(hipStream_t stream, int dtype, const void* qkv, int64_t rs, const float* q_dyt,
+                      const float* k_dyt, const float* cosT, const float* sinT, int half, int window, const float* lam,
+                      void* out, int B, int S, int H, int D, void* workspace) {
   using namespace band_tiled;
   const DenseLayout lay = band_tiled_layout(B, S, H, D);
   const int Sp = static_cast<int>(lay.Lp);
@@ -341,17 +344,15 @@ int launch_band_tiled(hipStream_t stream, const void* qkv, int64_t rs, const flo
   uint16_t* o = static_cast<uint16_t*>(out);
   const dim3 pgrid(static_cast<unsigned>(Sp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
   const int nblocks = B * H * ((S + 127) / 128);
-  if (D == 64) {
-    hipLaunchKernelGGL(band_prep_bf16<64>, pgrid, dim3(256), 0, stream, x, rs, k_dyt, cosT, sinT, half, S, Sp, H,
-                       lay.region_elems, ws);
-    hipLaunchKernelGGL(band_attend_bf16<64>, dim3(nblocks), dim3(256), 0, stream, x, rs, q_dyt, k_dyt, cosT, sinT,
-                       half, window, ws, lay.region_elems, B, S, Sp, H, lam, o);
-  } else {
-    hipLaunchKernelGGL(band_prep_bf16<128>, pgrid, dim3(256), 0, stream, x, rs, k_dyt, cosT, sinT, half, S, Sp, H,
-                       lay.region_elems, ws);
-    hipLaunchKernelGGL(band_attend_bf16<128>, dim3(nblocks), dim3(256), 0, stream, x, rs, q_dyt, k_dyt, cosT, sinT,
-                       half, window, ws, lay.region_elems, B, S, Sp, H, lam, o);
-  }
+  const bool f16 = dtype == HB_F16;
+  auto prep = D == 64 ? (f16 ? band_prep<F16Io, 64> : band_prep<Bf16Io, 64>)
+                      : (f16 ? band_prep<F16Io, 128> : band_prep<Bf16Io, 128>);
+  auto attend = D == 64 ? (f16 ? band_attend<F16Io, 64> : band_attend<Bf16Io, 64>)
+                        : (f16 ? band_attend<F16Io, 128> : band_attend<Bf16Io, 128>);
+  hipLaunchKernelGGL(prep, pgrid, dim3(256), 0, stream, x, rs, k_dyt, cosT, sinT, half, S, Sp, H, lay.region_elems,
+                     ws);
+  hipLaunchKernelGGL(attend, dim3(nblocks), dim3(256), 0, stream, x, rs, q_dyt, k_dyt, cosT, sinT, half, window, ws,
+                     lay.region_elems, B, S, Sp, H, lam, o);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(HB_ERR_LAUNCH, "band_tiled launch failed: %s", hipGetErrorString(e));
   return HB_OK;

@@ -28,6 +28,40 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// Element type of qkv and out (the compute dtype of the reference's bf16 and fp16 presets, sa3jax/dtypes.py:40-58).
+// The attention operands themselves (K, q * scale, P, V) are bf16 under both, as in the reference's fused kernels
+// (dense_attention.py:75-77, 83, 90; band_attention.py:85, 94, 101); the type sets how inputs are read, where the
+// compute-dtype casts of the norms round (dense_attention.py:66, 69) and how the output is written.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+struct Bf16Io {
+  __device__ static __forceinline__ void unpack8(u32x4 v, float (&x)[8]);
+  __device__ static __forceinline__ float round(float f);
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi);
+  // 8 input elements as 8 bf16 (the fused kernels' `.astype(bf16)` of V)
+  __device__ static __forceinline__ u32x4 to_bf16x8(u32x4 v) { return v; }
+};
+
+struct F16Io {
+  // The whole 16 bytes are reinterpreted at once: hipcc miscompiles __builtin_bit_cast of a single element v[i] of
+  // an ext_vector (every i read element 0).
+  __device__ static __forceinline__ void unpack8(u32x4 v, float (&x)[8]) {
+    const f16x8 h = __builtin_bit_cast(f16x8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
+  }
+  // IEEE half round to nearest even (v_cvt_f16_f32 in the default rounding mode)
+  __device__ static __forceinline__ float round(float f) { return static_cast<float>(static_cast<_Float16>(f)); }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    f16x2 h;
+    h[0] = static_cast<_Float16>(lo);
+    h[1] = static_cast<_Float16>(hi);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  __device__ static __forceinline__ u32x4 to_bf16x8(u32x4 v);
+};
+
 // 16-byte global load / store of 8 bf16.
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
@@ -44,6 +78,15 @@ __device__ __forceinline__ u32x4 pack8(const float (&x)[8]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(x[2 * i], x[2 * i + 1]);
   return v;
+}
+
+__device__ __forceinline__ void Bf16Io::unpack8(u32x4 v, float (&x)[8]) { hb::unpack8(v, x); }
+__device__ __forceinline__ float Bf16Io::round(float f) { return round_bf16(f); }
+__device__ __forceinline__ uint32_t Bf16Io::pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+__device__ __forceinline__ u32x4 F16Io::to_bf16x8(u32x4 v) {
+  float x[8];
+  unpack8(v, x);  // exact: every half is a float
+  return pack8(x);
 }
 
 __device__ __forceinline__ f32x16 mfma_bf16_32x32x16(u32x4 a, u32x4 b, f32x16 c) {

@@ -29,7 +29,8 @@ int check_stride(const char* what, int64_t row_stride, int64_t min_elems) {
 }
 
 int check_shape(int dtype, int B, int L, int Nk, int H, int D, float eps) {
-  if (dtype != HB_BF16 && dtype != HB_F32) return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0) or HB_F32 (1)", dtype);
+  if (dtype != HB_BF16 && dtype != HB_F32 && dtype != HB_F16)
+    return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0), HB_F32 (1) or HB_F16 (2)", dtype);
   if (D != 64 && D != 128) return fail(HB_ERR_HEAD_DIM, "head_dim %d is not 64 or 128", D);
   if (B < 1 || L < 1 || Nk < 1 || H < 1)
     return fail(HB_ERR_SHAPE, "need B, L, Nk, H >= 1 (B=%d, L=%d, Nk=%d, H=%d)", B, L, Nk, H);
@@ -53,7 +54,7 @@ int check_workspace(const void* ws, size_t bytes, size_t need) {
 extern "C" {
 
 size_t hb_cross_workspace_size(int dtype, int B, int Nk, int H, int D) {
-  if ((dtype != HB_BF16 && dtype != HB_F32) || B < 1 || Nk < 1 || H < 1 || (D != 64 && D != 128)) return 0;
+  if ((dtype != HB_BF16 && dtype != HB_F32 && dtype != HB_F16) || B < 1 || Nk < 1 || H < 1 || (D != 64 && D != 128)) return 0;
   return dense_layout(dtype, B, Nk, H, D).total_bytes;
 }
 
@@ -82,8 +83,8 @@ int hb_cross_prep(hipStream_t stream, const void* kv, int dtype, int64_t row_str
   if (dtype == HB_F32)
     return launch_dense_prep_f32(stream, kv, row_stride, kKSec, kKdSec, kVSec, k_weight, nullptr, nullptr, 0, nullptr,
                                  B, Nk, H, D, eps, lay, workspace);
-  return launch_dense_prep_bf16(stream, kv, row_stride, kKSec, kKdSec, kVSec, k_weight, nullptr, nullptr, 0, nullptr, B,
-                                Nk, H, D, eps, lay, workspace);
+  return launch_dense_prep_16bit(stream, dtype, kv, row_stride, kKSec, kKdSec, kVSec, k_weight, nullptr, nullptr, 0,
+                                 nullptr, B, Nk, H, D, eps, lay, workspace);
 }
 
 int hb_cross_attend(hipStream_t stream, const void* q, int dtype, int64_t row_stride, const float* q_weight,
@@ -105,8 +106,8 @@ int hb_cross_attend(hipStream_t stream, const void* q, int dtype, int64_t row_st
                                    out, B, L, Nk, H, D, lay);
   }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
-  return launch_dense_attend_bf16(stream, q, row_stride, kQdSec, q_weight, k_weight, nullptr, nullptr, 0, eps, lam, out,
-                                  B, L, Nk, H, D, lay, workspace);
+  return launch_dense_attend_16bit(stream, dtype, q, row_stride, kQdSec, q_weight, k_weight, nullptr, nullptr, 0, eps, lam,
+                                   out, B, L, Nk, H, D, lay, workspace);
 }
 
 }  // extern "C"

@@ -48,13 +48,14 @@ __device__ __forceinline__ SoftmaxPlan dense_plan(const float* __restrict__ qw, 
 // (L, half) fp32 tables; `half` is a multiple of 8 (checked on the host). Workspace regions: k', k_diff', V'^T.
 // `sk`, `skd`, `sv`: the sections of k, k_diff and v in a row of `qkv`, in units of H * D elements (self-attention
 // reads a to_qkv row [q | k | v | q_diff | k_diff], cross-attention a to_kv row [k | k_diff | v]).
-template <int D>
-__global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restrict__ qkv, int64_t rs, int sk, int skd,
-                                                       int sv, const float* __restrict__ kw,
-                                                       const float* __restrict__ cosT,
-                                                       const float* __restrict__ sinT, int half,
-                                                       const float* __restrict__ vmask, int L, int Lp, int H,
-                                                       float eps, int64_t region, uint16_t* __restrict__ ws) {
+// IO: the element type of qkv (bf16 or half); the RMSNorm and RoPE outputs round to it (the compute dtype,
+// dense_attention.py:66, 69) and then to bf16 for the workspace (75-77).
+template <class IO, int D>
+__global__ __launch_bounds__(256) void dense_prep(const uint16_t* __restrict__ qkv, int64_t rs, int sk, int skd, int sv,
+                                                  const float* __restrict__ kw, const float* __restrict__ cosT,
+                                                  const float* __restrict__ sinT, int half,
+                                                  const float* __restrict__ vmask, int L, int Lp, int H, float eps,
+                                                  int64_t region, uint16_t* __restrict__ ws) {
   constexpr int PAIRS = D / 16;            // group pairs per row; the lanes of one token are consecutive
   constexpr int TASKS = 64 * PAIRS / 256;  // (token, pair) tasks per thread
   constexpr int VCH = 64 * D / 8 / 256;    // 16-byte V chunks per thread
@@ -108,8 +109,8 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
 #pragma unroll
     for (int si = 0; si < 2; ++si) {
       float x1[8], x2[8];
-      unpack8(raw[i][si][0], x1);
-      unpack8(raw[i][si][1], x2);
+      IO::unpack8(raw[i][si][0], x1);
+      IO::unpack8(raw[i][si][1], x2);
       float ss = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss = __fmaf_rn(x2[j], x2[j], __fmaf_rn(x1[j], x1[j], ss));
@@ -119,8 +120,8 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
       float y1[8], y2[8], o1[8], o2[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {  // RMSNorm (dit.py:56-57): x * rsqrt(mean + eps), * w, cast
-        y1[j] = round_bf16((x1[j] * inv) * kw[8 * m1 + j]);
-        y2[j] = round_bf16((x2[j] * inv) * kw[8 * m2 + j]);
+        y1[j] = IO::round((x1[j] * inv) * kw[8 * m1 + j]);
+        y2[j] = IO::round((x2[j] * inv) * kw[8 * m2 + j]);
       }
       if (trot[i]) {
         const float c[8] = {cs[i][0][0], cs[i][0][1], cs[i][0][2], cs[i][0][3],
@@ -129,8 +130,8 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
                             cs[i][3][0], cs[i][3][1], cs[i][3][2], cs[i][3][3]};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {  // rotate_half (dit.py:96-98): d < half takes -x[d+half], else x[d-half]
-          o1[j] = round_bf16(y1[j] * c[j] + (-y2[j]) * s[j]);
-          o2[j] = round_bf16(y2[j] * c[j] + y1[j] * s[j]);
+          o1[j] = IO::round(y1[j] * c[j] + (-y2[j]) * s[j]);
+          o2[j] = IO::round(y2[j] * c[j] + y1[j] * s[j]);
         }
       } else {
 #pragma unroll
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
         for (int j = 0; j < 8; ++j) o1[j] = o2[j] = 0.f;
       }
       uint16_t* dst = ws + si * region + (bh * Lp + l) * D;
-      st16(dst + 8 * m1, pack8(o1));
+      st16(dst + 8 * m1, pack8(o1));  // bf16 (exact for bf16 IO; the fused kernel's second cast for half)
       st16(dst + 8 * m2, pack8(o2));
     }
   }
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(256) void dense_prep_bf16(const uint16_t* __restric
   for (int i = 0; i < VCH; ++i) {
     const int ch = t + 256 * i, key = ch / (D / 8), col = (ch % (D / 8)) * 8;
     float x[8];
-    unpack8(vraw[i], x);
+    IO::unpack8(vraw[i], x);
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] *= vm[i];
     *reinterpret_cast<u32x4*>(vt + vt_at(key, col)) = pack8(x);
@@ -238,11 +239,11 @@ __device__ __forceinline__ void dense_attend_loop(
 
 // RMSNorm (dit.py:45-57), rotate-half RoPE over the first 2 * 8 H8 dims (dit.py:90-98) and the softmax scale of
 // one query row, held whole by this lane: `row` points at its D elements in qkv, `cs` / `sn` at its (half)
-// columns of the tables. Cast points are those of the reference fused kernel: bf16 after the gain, after the
-// rotation and after the scale. The rotary width is a template parameter so that the partner of every dim is a
+// columns of the tables. Cast points are those of the reference fused kernel: the compute dtype IO after the gain
+// and after the rotation, bf16 after the scale. The rotary width is a template parameter so that the partner of every dim is a
 // fixed register. Rows at or past L are prepared from row L - 1 (the caller clamps `row`); their outputs are
 // never stored, and real rows keep the logits within the softmax plan's bound.
-template <int D, int H8>
+template <class IO, int D, int H8>
 __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, const float* __restrict__ qw,
                                            const float* __restrict__ cs, const float* __restrict__ sn, float eps,
                                            float qscale, u32x4 (&out)[D / 8]) {
@@ -264,18 +265,18 @@ __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, con
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < D / 8; ++c) {
-    unpack8(raw[c], *reinterpret_cast<float(*)[8]>(y + 8 * c));
+    IO::unpack8(raw[c], *reinterpret_cast<float(*)[8]>(y + 8 * c));
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss = __fmaf_rn(y[8 * c + j], y[8 * c + j], ss);
   }
   const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
 #pragma unroll
-  for (int d = 0; d < D; ++d) y[d] = round_bf16((y[d] * inv) * qw[d]);
+  for (int d = 0; d < D; ++d) y[d] = IO::round((y[d] * inv) * qw[d]);
 #pragma unroll
   for (int d = 0; d < 8 * H8; ++d) {  // d < half takes -x[d + half], d >= half takes x[d - half]
     const float y1 = y[d], y2 = y[d + 8 * H8];
-    y[d] = round_bf16(y1 * cv[d] + (-y2) * sv[d]);
-    y[d + 8 * H8] = round_bf16(y2 * cv[d] + y1 * sv[d]);
+    y[d] = IO::round(y1 * cv[d] + (-y2) * sv[d]);
+    y[d + 8 * H8] = IO::round(y2 * cv[d] + y1 * sv[d]);
   }
 #pragma unroll
   for (int c = 0; c < D / 8; ++c) {
@@ -289,8 +290,10 @@ __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, con
 // `qkv` rows hold q at section 0 and q_diff at section `sqd` (units of H * D); the L queries are padded to Lp (a
 // multiple of 128), the Lk keys of the workspace to Lkp. Self-attention has Lk = L. QB: queries per workgroup;
 // the 64-query form runs three workgroups per CU.
-template <int D, int QB>
-__global__ __launch_bounds__(256, D == 64 ? (QB == 64 ? 3 : 2) : 1) void dense_attend_bf16(
+// IO: the element type of qkv and out (bf16 or half); the attention operands are bf16 either way. QB: queries per
+// workgroup; the 64-query form runs three workgroups per CU.
+template <class IO, int D, int QB>
+__global__ __launch_bounds__(256, D == 64 ? (QB == 64 ? 3 : 2) : 1) void dense_attend(
     const uint16_t* __restrict__ qkv, int64_t rs, int sqd, const float* __restrict__ cosT,
     const float* __restrict__ sinT, int half, float eps, const uint16_t* __restrict__ ws, int64_t region, int B,
     int L, int Lp, int Lk, int Lkp, int H, const float* __restrict__ qw, const float* __restrict__ kw,
@@ -326,20 +329,20 @@ __global__ __launch_bounds__(256, D == 64 ? (QB == 64 ? 3 : 2) : 1) void dense_a
     const float* sn = sinT + static_cast<int64_t>(qc) * half;
     u32x4 whole[D / 8];
     switch (half / 8) {  // half % 8 == 0 and half <= D / 2 are checked on the host
-      case 0: prep_q_row<D, 0>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 1: prep_q_row<D, 1>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 2: prep_q_row<D, 2>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 3: prep_q_row<D, 3>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 0: prep_q_row<IO, D, 0>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 1: prep_q_row<IO, D, 1>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 2: prep_q_row<IO, D, 2>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 3: prep_q_row<IO, D, 3>(row, qw, cs, sn, eps, plan.qscale, whole); break;
       default:
         if constexpr (D == 64) {
-          prep_q_row<D, 4>(row, qw, cs, sn, eps, plan.qscale, whole);
+          prep_q_row<IO, D, 4>(row, qw, cs, sn, eps, plan.qscale, whole);
         } else {
           switch (half / 8) {
-            case 4: prep_q_row<D, 4>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 5: prep_q_row<D, 5>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 6: prep_q_row<D, 6>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 7: prep_q_row<D, 7>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-            default: prep_q_row<D, 8>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 4: prep_q_row<IO, D, 4>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 5: prep_q_row<IO, D, 5>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 6: prep_q_row<IO, D, 6>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 7: prep_q_row<IO, D, 7>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            default: prep_q_row<IO, D, 8>(row, qw, cs, sn, eps, plan.qscale, whole); break;
           }
         }
     }
@@ -381,7 +384,7 @@ __global__ __launch_bounds__(256, D == 64 ? (QB == 64 ? 3 : 2) : 1) void dense_a
   // Both stages are free once every wave is past its last tile; the exchange reuses them.
   static_assert(2 * NCT * (D / 32) * 16 * 64 * 4 <= 2 * T::STAGE * 2, "exchange buffer exceeds the two stages");
   if constexpr (T::SPLIT) __syncthreads();
-  store_diff_split<D, QB>(out, b, L, H, h, q0, br0, lam ? lam[h] : 1.f, o, lsum, smem);
+  store_diff_split<D, QB, IO>(out, b, L, H, h, q0, br0, lam ? lam[h] : 1.f, o, lsum, smem);
 }
 
 __global__ void rope_tables_kernel(const float* __restrict__ inv_freq, int half, int length, float* __restrict__ cosT,
@@ -443,30 +446,31 @@ static int dense_checks(const void* qkv, int dtype, int64_t row_stride, const fl
 
 namespace hb {
 
-int launch_dense_prep_bf16(hipStream_t stream, const void* kv, int64_t rs, int sk, int skd, int sv, const float* kw,
-                           const float* cos, const float* sin, int half, const float* vmask, int B, int Lk, int H,
-                           int D, float eps, const DenseLayout& lay, void* workspace) {
+int launch_dense_prep_16bit(hipStream_t stream, int dtype, const void* kv, int64_t rs, int sk, int skd, int sv,
+                            const float* kw, const float* cos, const float* sin, int half, const float* vmask, int B,
+                            int Lk, int H, int D, float eps, const DenseLayout& lay, void* workspace) {
   const dim3 grid(static_cast<unsigned>(lay.Lp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
   const uint16_t* x = static_cast<const uint16_t*>(kv);
   uint16_t* ws = static_cast<uint16_t*>(workspace);
   const int Lkp = static_cast<int>(lay.Lp);
-  if (D == 64)
-    hipLaunchKernelGGL(dense_prep_bf16<64>, grid, dim3(256), 0, stream, x, rs, sk, skd, sv, kw, cos, sin, half, vmask,
-                       Lk, Lkp, H, eps, lay.region_elems, ws);
-  else
-    hipLaunchKernelGGL(dense_prep_bf16<128>, grid, dim3(256), 0, stream, x, rs, sk, skd, sv, kw, cos, sin, half,
-                       vmask, Lk, Lkp, H, eps, lay.region_elems, ws);
+  const bool f16 = dtype == HB_F16;
+  auto kernel = D == 64 ? (f16 ? dense_prep<F16Io, 64> : dense_prep<Bf16Io, 64>)
+                        : (f16 ? dense_prep<F16Io, 128> : dense_prep<Bf16Io, 128>);
+  hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, x, rs, sk, skd, sv, kw, cos, sin, half, vmask, Lk, Lkp, H,
+                     eps, lay.region_elems, ws);
   return launch_status("dense_prep");
 }
 
-int launch_dense_attend_bf16(hipStream_t stream, const void* q, int64_t rs, int sqd, const float* qw, const float* kw,
-                             const float* cos, const float* sin, int half, float eps, const float* lam, void* out,
-                             int B, int L, int Lk, int H, int D, const DenseLayout& lay, const void* workspace) {
+int launch_dense_attend_16bit(hipStream_t stream, int dtype, const void* q, int64_t rs, int sqd, const float* qw,
+                              const float* kw, const float* cos, const float* sin, int half, float eps,
+                              const float* lam, void* out, int B, int L, int Lk, int H, int D, const DenseLayout& lay,
+                              const void* workspace) {
   const int Lp = (L + 127) / 128 * 128;
   const uint16_t* x = static_cast<const uint16_t*>(q);
   const uint16_t* ws = static_cast<const uint16_t*>(workspace);
   uint16_t* o = static_cast<uint16_t*>(out);
   const int Lkp = static_cast<int>(lay.Lp);
+  const bool f16 = dtype == HB_F16;
   // 128-query workgroups run two per CU. With between one and one and a half of them per CU, some CUs would run
   // two while most run one; 64-query workgroups (three per CU) spread the same work more evenly (measured: 6 %
   // faster at 288 workgroups on 256 CUs; slower at exactly one per CU and at nearly two, where they cost more per
@@ -475,16 +479,14 @@ int launch_dense_attend_bf16(hipStream_t stream, const void* q, int64_t rs, int 
   const int64_t ncu = device_cus();
   if (D == 64 && blocks128 > ncu && 2 * blocks128 <= 3 * ncu) {
     const int nblocks = B * H * (Lp / 64);
-    hipLaunchKernelGGL((dense_attend_bf16<64, 64>), dim3(nblocks), dim3(DenseTile<64, 64>::NT), 0, stream, x, rs, sqd,
-                       cos, sin, half, eps, ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw, lam, o);
-  } else if (D == 64) {
-    hipLaunchKernelGGL((dense_attend_bf16<64, 128>), dim3(static_cast<unsigned>(blocks128)), dim3(DenseTile<64>::NT),
-                       0, stream, x, rs, sqd, cos, sin, half, eps, ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw,
-                       lam, o);
+    auto kernel = f16 ? dense_attend<F16Io, 64, 64> : dense_attend<Bf16Io, 64, 64>;
+    hipLaunchKernelGGL(kernel, dim3(nblocks), dim3(DenseTile<64, 64>::NT), 0, stream, x, rs, sqd, cos, sin, half, eps,
+                       ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw, lam, o);
   } else {
-    hipLaunchKernelGGL((dense_attend_bf16<128, 128>), dim3(static_cast<unsigned>(blocks128)),
-                       dim3(DenseTile<128>::NT), 0, stream, x, rs, sqd, cos, sin, half, eps, ws, lay.region_elems, B, L,
-                       Lp, Lk, Lkp, H, qw, kw, lam, o);
+    auto kernel = D == 64 ? (f16 ? dense_attend<F16Io, 64, 128> : dense_attend<Bf16Io, 64, 128>)
+                          : (f16 ? dense_attend<F16Io, 128, 128> : dense_attend<Bf16Io, 128, 128>);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks128)), dim3(256), 0, stream, x, rs, sqd, cos, sin,
+                       half, eps, ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw, lam, o);
   }
   return launch_status("dense_attend");
 }
@@ -504,8 +506,8 @@ extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int
   if (dtype == HB_F32)
     return launch_dense_prep_f32(stream, qkv, row_stride, kSecK, kSecKd, kSecV, k_weight, cos, sin, half, vmask, B, L,
                                  H, D, eps, lay, workspace);
-  return launch_dense_prep_bf16(stream, qkv, row_stride, kSecK, kSecKd, kSecV, k_weight, cos, sin, half, vmask, B, L,
-                                H, D, eps, lay, workspace);
+  return launch_dense_prep_16bit(stream, dtype, qkv, row_stride, kSecK, kSecKd, kSecV, k_weight, cos, sin, half, vmask,
+                                 B, L, H, D, eps, lay, workspace);
 }
 
 extern "C" int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,
@@ -526,8 +528,8 @@ extern "C" int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, i
                                    B, L, L, H, D, lay);
   }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
-  return launch_dense_attend_bf16(stream, qkv, row_stride, kSecQd, q_weight, k_weight, cos, sin, half, eps, lam, out, B,
-                                  L, L, H, D, lay, workspace);
+  return launch_dense_attend_16bit(stream, dtype, qkv, row_stride, kSecQd, q_weight, k_weight, cos, sin, half, eps, lam,
+                                   out, B, L, L, H, D, lay, workspace);
 }
 
 extern "C" int hb_dense_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,

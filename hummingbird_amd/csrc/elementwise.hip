@@ -5,10 +5,10 @@
 //         to the compute dtype before the next GEMM, as the block does (same_l.py:191-192);
 //   glu   out = value * act(gate) for the glu_proj output [value | gate] (same_l._feed_forward, same_l.py:172-183),
 //         act = SiLU, or sin(pi * gate) on the sinusoidal blocks.
-// Both are single HBM passes: every thread moves 16-byte chunks (8 bf16 or 4 fp32 elements) of one row, the
-// per-channel parameters come from L1/L2. Cast points are the reference's: bf16 runs round where the XLA chain
-// holds a bf16 array (after the DyT; pi itself, pi * gate and the sine; the sigmoid and the SiLU; the product);
-// fp32 runs do not round.
+// Both are single HBM passes: every thread moves 16-byte chunks (8 bf16 or half, or 4 fp32 elements) of one row,
+// the per-channel parameters come from L1/L2. Cast points are the reference's: bf16 and half runs round where the
+// XLA chain holds an array of the compute dtype (after the DyT; pi itself, pi * gate and the sine; the sigmoid and
+// the SiLU; the product); fp32 runs do not round.
 #include "api.h"
 #include "common.h"
 
@@ -20,13 +20,28 @@ struct Vec;
 template <>
 struct Vec<uint16_t> {  // bf16: 8 elements per 16 bytes
   static constexpr int N = 8;
+  static constexpr bool kHwSine = true;
   __device__ static void load(const uint16_t* p, float (&x)[8]) { unpack8(ld16(p), x); }
   __device__ static void store(uint16_t* p, const float (&x)[8]) { st16(p, pack8(x)); }
   __device__ static float round(float x) { return round_bf16(x); }
 };
 template <>
+struct Vec<_Float16> {  // IEEE half (the fp16 preset): 8 elements per 16 bytes
+  static constexpr int N = 8;
+  static constexpr bool kHwSine = false;  // half's 11 bits need the library sine near the zeros of sin(pi g)
+  __device__ static void load(const _Float16* p, float (&x)[8]) { F16Io::unpack8(ld16(p), x); }
+  __device__ static void store(_Float16* p, const float (&x)[8]) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = F16Io::pack2(x[2 * i], x[2 * i + 1]);
+    st16(p, v);
+  }
+  __device__ static float round(float x) { return F16Io::round(x); }
+};
+template <>
 struct Vec<float> {  // fp32: 4 elements per 16 bytes
   static constexpr int N = 4;
+  static constexpr bool kHwSine = false;
   __device__ static void load(const float* p, float (&x)[4]) {
     const f32x4 v = *reinterpret_cast<const f32x4*>(p);
     for (int i = 0; i < 4; ++i) x[i] = v[i];
@@ -90,7 +105,7 @@ __global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ proj, in
       float act;
       if constexpr (SINE) {
         const float t = Vec<T>::round(Vec<T>::round(static_cast<float>(M_PI)) * g[i]);
-        if constexpr (Vec<T>::N == 8) {
+        if constexpr (Vec<T>::kHwSine) {
           // bf16: Cody-Waite reduction of t by 2 pi = C1 + C2 (C1 = 6.28125 has 8 significant bits, so k * C1 is
           // exact for |k| < 2^16), then the hardware sine (v_sin_f32, argument in revolutions) of the remainder,
           // |rev| <= 1/2. Its error is far inside the bf16 rounding of the result. Larger |t| take the library sine.
@@ -123,9 +138,10 @@ namespace {
 
 int check_rows(const char* what, int dtype, const void* in, int64_t in_stride, const void* out, int64_t out_stride,
                int64_t N, int C, int64_t in_min) {
-  if (dtype != HB_BF16 && dtype != HB_F32) return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0) or HB_F32 (1)", dtype);
+  if (dtype != HB_BF16 && dtype != HB_F32 && dtype != HB_F16)
+    return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0), HB_F32 (1) or HB_F16 (2)", dtype);
   if (N < 1 || C < 1 || N > (int64_t(1) << 31)) return fail(HB_ERR_SHAPE, "%s needs 1 <= N <= 2^31 and C >= 1", what);
-  const int vec = dtype == HB_BF16 ? 8 : 4;
+  const int vec = dtype == HB_F32 ? 4 : 8;
   if (C % vec) return fail(HB_ERR_SHAPE, "%s needs the channel count (%d) to be a multiple of %d", what, C, vec);
   if (in_stride < in_min || out_stride < C || in_stride % vec || out_stride % vec)
     return fail(HB_ERR_STRIDE, "%s row strides (%lld, %lld) must be >= (%lld, %d) and multiples of %d", what,
@@ -159,10 +175,14 @@ int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, c
   int st = check_rows("dyt", dtype, x, x_row_stride, out, out_row_stride, N, C, C);
   if (st) return st;
   if (!dyt) return fail(HB_ERR_NULL, "dyt parameters must be non-NULL");
-  const int chunks = C / (dtype == HB_BF16 ? 8 : 4);
+  const int chunks = C / (dtype == HB_F32 ? 4 : 8);
   if (dtype == HB_BF16)
     hipLaunchKernelGGL(ew::dyt_kernel<uint16_t>, row_grid(N, chunks), dim3(256), 0, stream,
                        static_cast<const uint16_t*>(x), x_row_stride, dyt, static_cast<uint16_t*>(out), out_row_stride,
+                       N, C);
+  else if (dtype == HB_F16)
+    hipLaunchKernelGGL(ew::dyt_kernel<_Float16>, row_grid(N, chunks), dim3(256), 0, stream,
+                       static_cast<const _Float16*>(x), x_row_stride, dyt, static_cast<_Float16*>(out), out_row_stride,
                        N, C);
   else
     hipLaunchKernelGGL(ew::dyt_kernel<float>, row_grid(N, chunks), dim3(256), 0, stream, static_cast<const float*>(x),
@@ -175,9 +195,18 @@ int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_str
   clear_error();
   int st = check_rows("glu", dtype, proj, proj_row_stride, out, out_row_stride, N, F, static_cast<int64_t>(2) * F);
   if (st) return st;
-  const int chunks = F / (dtype == HB_BF16 ? 8 : 4);
+  const int chunks = F / (dtype == HB_F32 ? 4 : 8);
   const dim3 grid = row_grid(N, chunks);
-  if (dtype == HB_BF16) {
+  if (dtype == HB_F16) {
+    const _Float16* p = static_cast<const _Float16*>(proj);
+    _Float16* o = static_cast<_Float16*>(out);
+    if (sinusoidal)
+      hipLaunchKernelGGL((ew::glu_kernel<_Float16, true>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
+    else
+      hipLaunchKernelGGL((ew::glu_kernel<_Float16, false>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
+  } else if (dtype == HB_BF16) {
     const uint16_t* p = static_cast<const uint16_t*>(proj);
     uint16_t* o = static_cast<uint16_t*>(out);
     if (sinusoidal)

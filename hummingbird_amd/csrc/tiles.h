@@ -92,11 +92,11 @@ struct TileCopy {
 };
 
 // out[q, h*D + d] = O1 / l1 - lam * O2 / l2 for the QB queries of a 4-wave workgroup laid out as DenseTile<D, QB>
-// describes (q0w: this wave's first query, br0: its first branch), written as bf16 for q < N.
+// describes (q0w: this wave's first query, br0: its first branch), written in the output type IO for q < N.
 // D = 64: the branch-2 waves publish lam * O2 / l2 (rounded per element) through LDS (`xbuf_mem`, at least
 // 32 KB, free of tile reads: the caller has passed a barrier after its last tile) and the branch-1 waves
 // subtract it from O1 / l1; D = 128: each wave holds both branches. Every lane of the workgroup must call it.
-template <int D, int QB = 128>
+template <int D, int QB = 128, class IO = Bf16Io>
 __device__ __forceinline__ void store_diff_split(uint16_t* __restrict__ out, int64_t b, int N, int H, int h, int q0w,
                                                  int br0, float lamh,
                                                  const f32x16 (&o)[DenseTile<D, QB>::NB][DenseTile<D, QB>::NCT][D / 32],
@@ -139,8 +139,8 @@ __device__ __forceinline__ void store_diff_split(uint16_t* __restrict__ out, int
             }
             if (q < N) {
               u32x2 pk;
-              pk[0] = pack_bf16x2(v[0], v[1]);
-              pk[1] = pack_bf16x2(v[2], v[3]);
+              pk[0] = IO::pack2(v[0], v[1]);
+              pk[1] = IO::pack2(v[2], v[3]);
               *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * g + 4 * lh) = pk;
             }
           }
@@ -151,7 +151,7 @@ __device__ __forceinline__ void store_diff_split(uint16_t* __restrict__ out, int
     for (int ct = 0; ct < NCT; ++ct) {
       const int q = q0w + 32 * ct + lr;
       uint16_t* orow = q < N ? out + (b * N + q) * HD + h * D : nullptr;
-      store_diff_bf16<D, NCT>(orow, o, lsum, ct, lamh);
+      store_diff_bf16<D, NCT, IO>(orow, o, lsum, ct, lamh);
     }
   }
 }

@@ -11,17 +11,21 @@ from __future__ import annotations
 import torch
 
 from hummingbird_amd import _lib
-from hummingbird_amd._lib import HB_BF16, HB_F32
+from hummingbird_amd._lib import HB_BF16, HB_F16, HB_F32
 
 SUPPORTED_HEAD_DIMS = (64, 128)
 
+# The compute dtypes of the reference's presets (sa3jax/dtypes.py:40-58): BF16, FP16 and FP32_PARITY.
+_DTYPE_CODES = {torch.bfloat16: HB_BF16, torch.float16: HB_F16, torch.float32: HB_F32}
+
 
 def dtype_code(dtype: torch.dtype) -> int:
-    if dtype == torch.bfloat16:
-        return HB_BF16
-    if dtype == torch.float32:
-        return HB_F32
-    raise TypeError(f"hummingbird_amd kernels take bfloat16 or float32 inputs, got {dtype}")
+    """The C ABI's code for a compute dtype: bf16, fp16 (both with bf16 attention operands, as the reference's
+    fused kernels) or fp32."""
+    code = _DTYPE_CODES.get(dtype)
+    if code is None:
+        raise TypeError(f"hummingbird_amd kernels take bfloat16, float16 or float32 inputs, got {dtype}")
+    return code
 
 
 def _require_gpu(t: torch.Tensor, name: str) -> None:

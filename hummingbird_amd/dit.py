@@ -13,6 +13,7 @@ import torch
 from hummingbird_amd import cross_attention as xattn
 from hummingbird_amd import dense_attention, xla_chain
 from hummingbird_amd.config import DiTConfig
+from hummingbird_amd.dtypes import Dtype
 
 
 def use_hip(cfg: DiTConfig, qkv: torch.Tensor) -> bool:
@@ -27,9 +28,12 @@ def use_hip(cfg: DiTConfig, qkv: torch.Tensor) -> bool:
 
 
 def static_tables(inv_freq: torch.Tensor, valid: torch.Tensor, cfg: DiTConfig,
-                  compute: torch.dtype) -> dict[str, torch.Tensor]:
+                  compute: torch.dtype | Dtype) -> dict[str, torch.Tensor]:
     """Per-clip tables (reference: dit._static, dit.py:317-336). `valid` is the `(B, T)` padding mask of the
-    latents; the mask is extended over the memory tokens (dit.py:320)."""
+    latents; the mask is extended over the memory tokens (dit.py:320). `compute` is the compute dtype or a `Dtype`
+    preset."""
+    if isinstance(compute, Dtype):
+        compute = compute.compute
     batch = valid.shape[0]
     ones = torch.ones((batch, cfg.num_memory_tokens), dtype=torch.bool, device=valid.device)
     full = torch.cat([ones, valid.to(torch.bool)], dim=-1)
@@ -42,11 +46,15 @@ def static_tables(inv_freq: torch.Tensor, valid: torch.Tensor, cfg: DiTConfig,
 
 
 def self_attention(h: torch.Tensor, block: dict, static: dict, cfg: DiTConfig,
-                   lam: torch.Tensor | None = None) -> torch.Tensor:
+                   lam: torch.Tensor | None = None, dtype: Dtype | None = None) -> torch.Tensor:
     """`to_qkv` -> differential self-attention -> `to_out` (reference: dit._self_attention, dit.py:185-200).
-    `block["self_attn"]` holds `to_qkv.weight (5E, E)`, `to_out.weight (E, E)`, `q_norm.weight`, `k_norm.weight`."""
+    `block["self_attn"]` holds `to_qkv.weight (5E, E)`, `to_out.weight (E, E)`, `q_norm.weight`, `k_norm.weight`.
+    `dtype` (a preset of hummingbird_amd.dtypes, as the reference's `dtype` argument) casts `h` and the projection
+    weights to its compute dtype; without it they are used as given."""
     attn = block["self_attn"]
-    qkv = h @ attn["to_qkv"]["weight"].t()
+    if dtype is not None:
+        h = h.to(dtype.compute)
+    qkv = h @ attn["to_qkv"]["weight"].to(h.dtype).t()
     if use_hip(cfg, qkv):
         out = dense_attention.dense_attention(qkv, attn["q_norm"]["weight"], attn["k_norm"]["weight"],
                                               static["hip_cos"], static["hip_sin"], static["hip_mask"],
@@ -57,7 +65,7 @@ def self_attention(h: torch.Tensor, block: dict, static: dict, cfg: DiTConfig,
             raise NotImplementedError("only the differential self-attention is on this package's path")
         out = xla_chain.dense_chain(qkv, attn["q_norm"]["weight"], attn["k_norm"]["weight"], static["inv_freq"],
                                     static["valid"], cfg.num_heads, cfg.head_dim, cfg.qk_norm_eps, lam=lam)
-    return out @ attn["to_out"]["weight"].t()
+    return out @ attn["to_out"]["weight"].to(out.dtype).t()
 
 
 def cross_context(block: dict, ctx: torch.Tensor, cfg: DiTConfig):

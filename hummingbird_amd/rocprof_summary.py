@@ -26,13 +26,19 @@ from pathlib import Path
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
 
+IO_SUFFIX = {"hb::Bf16Io": "_bf16", "hb::F16Io": "_f16"}
+
+
 def short_name(name: str) -> str:
-    """``void hb::dense_attend_bf16<64, 128>(...)`` -> ``dense_attend_bf16<64,128>`` (also through nested
-    namespaces: ``hb::band_ring::band_ring_bf16<2>`` -> ``band_ring_bf16<2>``); other kernels keep a short
-    prefix."""
-    m = re.search(r"hb::(?:\w+::)*(\w+)(<\d+(?:,\s*\d+)*>)?", name)
+    """``void hb::dense_attend<hb::Bf16Io, 64, 128>(...)`` -> ``dense_attend_bf16<64,128>`` (the element type of
+    the kernel's inputs becomes a suffix; also through nested namespaces: ``hb::band_ring::band_ring<hb::Bf16Io, 2>``
+    -> ``band_ring_bf16<2>``; ``hb::dense_attend_f32<64>`` stays as it is); other kernels keep a short prefix."""
+    m = re.search(r"hb::(?:\w+::)*(\w+)(?:<([^()<>]*)>)?", name)
     if m:
-        return m.group(1) + re.sub(r"\s+", "", m.group(2) or "")
+        base, args = m.group(1), [a.strip() for a in (m.group(2) or "").split(",") if a.strip()]
+        if args and args[0] in IO_SUFFIX:
+            base, args = base + IO_SUFFIX[args[0]], args[1:]
+        return base + (f"<{','.join(args)}>" if args else "")
     return name.split("(")[0][:60]
 
 

@@ -10,6 +10,7 @@ import torch
 
 from hummingbird_amd import band_attention, elementwise, xla_chain
 from hummingbird_amd.config import SameConfig
+from hummingbird_amd.dtypes import Dtype
 
 
 def use_hip(cfg: SameConfig, qkv: torch.Tensor) -> bool:
@@ -21,19 +22,23 @@ def use_hip(cfg: SameConfig, qkv: torch.Tensor) -> bool:
     return True
 
 
-def attention(x: torch.Tensor, block: dict, cfg: SameConfig, lam: torch.Tensor | None = None) -> torch.Tensor:
+def attention(x: torch.Tensor, block: dict, cfg: SameConfig, lam: torch.Tensor | None = None,
+              dtype: Dtype | None = None) -> torch.Tensor:
     """`to_qkv` -> differential band attention at half-width `sub_chunk_size` -> `to_out` (reference:
     same_l._attention, same_l.py:151-169). `block` holds `self_attn.{to_qkv,to_out}.weight`,
-    `self_attn.{q_norm,k_norm}` DyT params and `rope_inv_freq`."""
+    `self_attn.{q_norm,k_norm}` DyT params and `rope_inv_freq`. `dtype` (a preset of hummingbird_amd.dtypes) casts
+    `x` and the projection weights to its compute dtype; without it they are used as given."""
     attn = block["self_attn"]
-    qkv = x @ attn["to_qkv"]["weight"].t()
+    if dtype is not None:
+        x = x.to(dtype.compute)
+    qkv = x @ attn["to_qkv"]["weight"].to(x.dtype).t()
     if use_hip(cfg, qkv):
         out = band_attention.band_attention(qkv, attn["q_norm"], attn["k_norm"], block["rope_inv_freq"],
                                             cfg.num_heads, cfg.dim_heads, cfg.sub_chunk_size, lam=lam)
     else:
         out = xla_chain.band_chain(qkv, attn["q_norm"], attn["k_norm"], block["rope_inv_freq"], cfg.num_heads,
                                    cfg.dim_heads, cfg.sub_chunk_size, lam=lam)
-    return out @ attn["to_out"]["weight"].t()
+    return out @ attn["to_out"]["weight"].to(out.dtype).t()
 
 
 def _linear(x: torch.Tensor, layer: dict) -> torch.Tensor:

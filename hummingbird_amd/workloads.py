@@ -35,15 +35,22 @@ def _bf16(x: np.ndarray) -> np.ndarray:
     return ((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
 
 
+def _as(x: np.ndarray, dtype: str) -> np.ndarray:
+    """float32 values of the input dtype: 'bf16' and 'fp16' round to nearest even, 'fp32' keeps them."""
+    if dtype == "bf16":
+        return _bf16(x)
+    if dtype == "fp16":
+        return x.astype(np.float16).astype(np.float32)
+    return x
+
+
 def dense_inputs(batch: int, length: int, heads: int, head_dim: int, seed: int = 0, dtype: str = "bf16",
                  half: int | None = None, mask_tail: int = 16, ragged: bool = False, gain_std: float = 0.02,
                  gain_mean: float = 1.0) -> dict:
-    """Dense workload inputs as float32 NumPy arrays (qkv holds bf16 values when dtype == 'bf16')."""
+    """Dense workload inputs as float32 NumPy arrays (qkv holds values of `dtype`: 'bf16', 'fp16' or 'fp32')."""
     rng = np.random.default_rng(seed)
     half = head_dim // 2 if half is None else half
-    qkv = rng.standard_normal((batch, length, 5 * heads * head_dim), dtype=np.float32)
-    if dtype == "bf16":
-        qkv = _bf16(qkv)
+    qkv = _as(rng.standard_normal((batch, length, 5 * heads * head_dim), dtype=np.float32), dtype)
     q_weight = (gain_mean + gain_std * rng.standard_normal(head_dim)).astype(np.float32)
     k_weight = (gain_mean + gain_std * rng.standard_normal(head_dim)).astype(np.float32)
     lam = rng.uniform(0.2, 0.8, heads).astype(np.float32)
@@ -61,12 +68,10 @@ def dense_inputs(batch: int, length: int, heads: int, head_dim: int, seed: int =
 
 def band_inputs(batch: int, length: int, heads: int, head_dim: int, window: int, seed: int = 1,
                 dtype: str = "bf16", half: int | None = None, alpha: float = 0.5, gamma_mean: float = 1.0) -> dict:
-    """Band workload inputs as float32 NumPy arrays (qkv holds bf16 values when dtype == 'bf16')."""
+    """Band workload inputs as float32 NumPy arrays (qkv holds values of `dtype`: 'bf16', 'fp16' or 'fp32')."""
     rng = np.random.default_rng(seed)
     half = head_dim // 2 if half is None else half
-    qkv = rng.standard_normal((batch, length, 5 * heads * head_dim), dtype=np.float32)
-    if dtype == "bf16":
-        qkv = _bf16(qkv)
+    qkv = _as(rng.standard_normal((batch, length, 5 * heads * head_dim), dtype=np.float32), dtype)
 
     def dyt():
         gamma = (gamma_mean + 0.02 * rng.standard_normal(head_dim)).astype(np.float32)
@@ -82,12 +87,11 @@ def band_inputs(batch: int, length: int, heads: int, head_dim: int, window: int,
 
 def cross_inputs(batch: int, length: int, context: int, heads: int, head_dim: int, seed: int = 0,
                  dtype: str = "bf16", gain_std: float = 0.02, gain_mean: float = 1.0) -> dict:
-    """Cross-attention inputs as float32 NumPy arrays (q and kv hold bf16 values when dtype == 'bf16')."""
+    """Cross-attention inputs as float32 NumPy arrays (q and kv hold values of `dtype`)."""
     rng = np.random.default_rng(seed)
     q = rng.standard_normal((batch, length, 2 * heads * head_dim), dtype=np.float32)
     kv = rng.standard_normal((batch, context, 3 * heads * head_dim), dtype=np.float32)
-    if dtype == "bf16":
-        q, kv = _bf16(q), _bf16(kv)
+    q, kv = _as(q, dtype), _as(kv, dtype)
     q_weight = (gain_mean + gain_std * rng.standard_normal(head_dim)).astype(np.float32)
     k_weight = (gain_mean + gain_std * rng.standard_normal(head_dim)).astype(np.float32)
     lam = rng.uniform(0.2, 0.8, heads).astype(np.float32)

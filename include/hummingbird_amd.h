@@ -44,7 +44,7 @@ enum hb_status {
   HB_OK = 0,
   HB_ERR_NULL = 1,      /* a required pointer is NULL */
   HB_ERR_SHAPE = 2,     /* B, N or H out of range */
-  HB_ERR_DTYPE = 3,     /* dtype is not HB_BF16 or HB_F32 */
+  HB_ERR_DTYPE = 3,     /* dtype is not HB_BF16, HB_F32 or HB_F16 */
   HB_ERR_HEAD_DIM = 4,  /* D is not 64 or 128 */
   HB_ERR_HALF = 5,      /* rotary half-width outside [0, D/2] or not a multiple of 8 */
   HB_ERR_WINDOW = 6,    /* band half-width < 0 */
@@ -54,7 +54,13 @@ enum hb_status {
   HB_ERR_EPS = 10       /* eps < 0 or not finite */
 };
 
-enum hb_dtype { HB_BF16 = 0, HB_F32 = 1 };
+/* The element type of the 16- or 32-bit inputs and outputs: the compute dtype of the reference's presets
+ * (sa3jax/dtypes.py:40-58). HB_BF16 is the bf16 preset and HB_F16 the fp16 preset; under both the attention
+ * operands (K, q * scale, P, V) are rounded to bf16 as in the reference's fused kernels
+ * (sa3jax/dense_attention.py:75-77, 83, 90; sa3jax/band_attention.py:85, 94, 101), while the RMSNorm and RoPE
+ * outputs round to the compute dtype (sa3jax/dense_attention.py:66, 69) and the output is written in it. HB_F32
+ * is the FP32_PARITY preset: fp32 throughout (the XLA chain's arithmetic). */
+enum hb_dtype { HB_BF16 = 0, HB_F32 = 1, HB_F16 = 2 };
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* hb_last_error(void);
@@ -81,7 +87,7 @@ int hb_rope_tables(hipStream_t stream, const float* inv_freq, int half, int leng
  *   q_weight, k_weight : D floats (RMSNorm scales)
  *   cos, sin           : (L, half) floats from hb_rope_tables (ignored when half == 0)
  *   vmask              : (B, L) floats, or NULL for all ones
- *   dtype              : HB_BF16 or HB_F32 (of qkv and out)
+ *   dtype              : HB_BF16, HB_F16 or HB_F32 (of qkv and out)
  *   D                  : 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  eps >= 0
  *   workspace          : >= hb_dense_workspace_size(dtype, B, L, H, D) bytes, 256-byte aligned; holds the
  *                        prepared k, k_diff and v for the duration of the call (stream-ordered).
@@ -127,11 +133,11 @@ int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, int64_t row_
  * half-width (`|k - q| <= window`, sa3jax/band_attention.py:110).
  *   q_dyt, k_dyt : 1 + 2*D floats each: [alpha, gamma[0..D), beta[0..D)]
  *   cos, sin     : (S, half) floats from hb_rope_tables (ignored when half == 0)
- *   dtype        : HB_BF16 or HB_F32;  D: 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  window >= 0
+ *   dtype        : HB_BF16, HB_F16 or HB_F32;  D: 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  window >= 0
  *   workspace    : >= hb_band_workspace_size(dtype, B, S, H, D, half, window) bytes, 256-byte aligned; that size
- *                  is 0 (and workspace may be NULL) for fp32 and for bf16 with D = 64 and window <= 128, which
+ *                  is 0 (and workspace may be NULL) for fp32 and for 16-bit inputs with D = 64 and window <= 128, which
  *                  run without one. Otherwise it holds the prepared keys for the duration of the call.
- * Kernels: bf16 with D = 64 and window <= 128 runs one streaming kernel; other bf16 shapes run a key
+ * Kernels: 16-bit inputs with D = 64 and window <= 128 run one streaming kernel; other 16-bit shapes run a key
  * preparation kernel and an attention kernel over the workspace; fp32 runs one kernel. */
 size_t hb_band_workspace_size(int dtype, int B, int S, int H, int D, int half, int window);
 int hb_band_validate(int dtype, int64_t row_stride, int B, int S, int H, int D, int half, int window);
@@ -151,7 +157,7 @@ int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row
  * over all Nk context keys: no RoPE and no mask (sa3jax/dit.py:204-205, 214-215).
  *   q      : (B, L, >= 2*H*D) with row stride `row_stride` (a multiple of 8), 16-byte aligned
  *   kv     : (B, Nk, >= 3*H*D) with row stride `row_stride` (a multiple of 8), 16-byte aligned
- *   dtype  : HB_BF16 or HB_F32 (of q, kv and out);  D: 64 or 128;  eps >= 0
+ *   dtype  : HB_BF16, HB_F16 or HB_F32 (of q, kv and out);  D: 64 or 128;  eps >= 0
  *   workspace : >= hb_cross_workspace_size(dtype, B, Nk, H, D) bytes, 256-byte aligned.
  * hb_cross_prep writes the prepared k, k_diff and v of the context into the workspace; hb_cross_attend reads
  * them, for as many query sets as the caller has (the reference computes them once per clip and reuses them in
@@ -172,12 +178,14 @@ int hb_cross_attend(hipStream_t stream, const void* q, int dtype, int64_t row_st
  *            `dyt` = [alpha, gamma[0..C), beta[0..C)].
  *   hb_glu : out[n, f] = value * act(gate) with [value | gate] = [proj[n, 0:F] | proj[n, F:2F]]
  *            (same_l._feed_forward, sa3jax/same_l.py:172-183); act = SiLU(gate) = gate * sigmoid(gate), or
- *            sin(pi * gate) when `sinusoidal` != 0. For bf16 the intermediate arrays of the XLA chain are rounded
- *            to bf16 where it holds them (the sigmoid and the SiLU; pi, pi * gate and the sine). `bias` (2F floats
- *            holding values of the compute dtype, or NULL) is the glu_proj layer's bias: proj holds the bare matmul
- *            and the bias is added first, rounded to the compute dtype as same_l._linear holds it.
- *   x, proj, out : N rows with row strides in elements (multiples of 8 for bf16, 4 for fp32), 16-byte aligned;
- *                  C and F multiples of 8 (bf16) or 4 (fp32);  dtype: HB_BF16 or HB_F32 (input and output). */
+ *            sin(pi * gate) when `sinusoidal` != 0. For bf16 and half the intermediate arrays of the XLA chain are
+ *            rounded to the compute dtype where it holds them (the sigmoid and the SiLU; pi, pi * gate and the sine).
+ *            `bias` (2F floats holding values of the compute dtype, or NULL) is the glu_proj layer's bias: proj
+ *            holds the bare matmul and the bias is added first, rounded to the compute dtype as same_l._linear
+ *            holds it.
+ *   x, proj, out : N rows with row strides in elements (multiples of 8 for bf16 and half, 4 for fp32), 16-byte
+ *                  aligned; C and F multiples of 8 (bf16, half) or 4 (fp32);  dtype: HB_BF16, HB_F16 or HB_F32 (input
+ *                  and output). */
 int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const float* dyt, void* out,
            int64_t out_row_stride, int64_t N, int C);
 int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_stride, const float* bias,

@@ -65,7 +65,7 @@ def dense_validate(lib, **kw):
     ({"D": 128, "H": 12, "row_stride": 5 * 12 * 128, "half": 64}, 0),
     ({"D": 96}, 4),                       # head_dim (reference: dense_attention.py:119-120)
     ({"half": 33}, 5), ({"half": -1}, 5),
-    ({"dtype": 7}, 3),
+    ({"dtype": 7}, 3), ({"dtype": 2}, 0),  # HB_F16: the reference's FP16 preset (dtypes.py:50-58)
     ({"row_stride": 100}, 7), ({"row_stride": 5 * 24 * 64 + 4}, 7),
     ({"L": 0}, 2), ({"B": 0}, 2), ({"H": 0}, 2),
     ({"eps": -1.0}, 10), ({"eps": float("nan")}, 10),
@@ -88,6 +88,7 @@ def test_band_validate(lib, kw, status):
 def test_workspace_size(lib):
     # three (B, H, Lp, D) regions (k, k_diff, v prepared) with L padded to the 128-query block
     assert lib.hb_dense_workspace_size(0, 2, 2584, 24, 64) == 3 * 2 * 24 * 2688 * 64 * 2
+    assert lib.hb_dense_workspace_size(2, 2, 2584, 24, 64) == 3 * 2 * 24 * 2688 * 64 * 2  # half: bf16 operands
     assert lib.hb_dense_workspace_size(1, 1, 1, 1, 64) == 3 * 128 * 64 * 4
     assert lib.hb_dense_workspace_size(0, 1, 1, 1, 96) == 0
 

@@ -269,4 +269,4 @@ def test_dense_errors_are_value_errors():
     with pytest.raises(ValueError):
         da.dense_attention(qkv, w, w, None, None, None, 2, 64, 40, 1e-6)
     with pytest.raises(TypeError):
-        da.dense_attention(qkv.half(), w, w, None, None, None, 2, 64, 0, 1e-6)
+        da.dense_attention(qkv.double(), w, w, None, None, None, 2, 64, 0, 1e-6)
