@@ -61,48 +61,88 @@ def parse() -> argparse.Namespace:
     return ap.parse_args()
 
 
+def _median_time(fn, target_s: float, min_runs: int = 5) -> tuple[float, int]:
+    """Median wall time (s) of warm runs of `fn`: at least `min_runs`, more until about `target_s` has passed."""
+    fn()  # warm
+    times = []
+    t_end = time.perf_counter() + target_s
+    while len(times) < min_runs or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def config0_inputs(seed: int = 0) -> dict:
+    """The CPU configuration: x ~ N(0,1) (1, 216, 1536); W_qkv (7680, 1536) and W_o (1536, 1536) ~ N(0, 1/1536);
+    RMSNorm gains ~ 1 + N(0, 0.02); RoPE base 10000 over the full head_dim (half 32); per-pair lambda ~ U(0.2, 0.8);
+    value mask ones except the last 16 tokens; 24 heads of 64; seed 0."""
+    rng = np.random.default_rng(seed)
+    E, L, H, D = 1536, 216, 24, 64
+    x = rng.standard_normal((1, L, E), dtype=np.float32)
+    w_qkv = (rng.standard_normal((5 * E, E)) / np.sqrt(E)).astype(np.float32)
+    w_o = (rng.standard_normal((E, E)) / np.sqrt(E)).astype(np.float32)
+    qw = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
+    kw = (1 + 0.02 * rng.standard_normal(D)).astype(np.float32)
+    lam = rng.uniform(0.2, 0.8, H).astype(np.float32)
+    valid = np.ones((1, L), np.float32)
+    valid[:, L - 16:] = 0.0
+    from hummingbird_amd import workloads as wl
+    return dict(x=x, w_qkv=w_qkv, w_o=w_o, q_weight=qw, k_weight=kw, lam=lam, valid=valid, inv_freq=wl.inv_freq(32),
+                heads=H, head_dim=D)
+
+
 def cpu_baseline(target_s: float) -> dict:
-    """Time the oracle (NumPy restatement of the reference XLA chains, fp32 accumulation) on a bounded sample
-    of the clip's work and scale it to ms per clip."""
+    """The oracle (NumPy restatement of the reference XLA chains, fp32 with fp32 accumulation, as XLA:CPU runs them)
+    on this host: config 0 whole (to_qkv -> attention -> to_out at L=216), and bounded samples of configs 1 and 2
+    (one of the 48 (batch, head) pairs of a dense call; one of the 8 band heads over 16384 of the 82688 frames),
+    each the median of at least 5 warm runs, scaled to a call and to one clip."""
     from threadpoolctl import threadpool_info
 
     from hummingbird_amd import workloads as wl
     from oracle import band as oband
     from oracle import dense as odense
 
+    rows = {}
+    # config 0, whole: no sampling
+    c0 = config0_inputs()
+
+    def config0():
+        qkv = (c0["x"] @ c0["w_qkv"].T).astype(np.float32)
+        out = odense.dense_xla(qkv, c0["q_weight"], c0["k_weight"], c0["inv_freq"], c0["valid"], c0["heads"],
+                               c0["head_dim"], 1e-6, c0["lam"], "fp32", np.float32)
+        return (out @ c0["w_o"].T).astype(np.float32)
+
+    t0, n0 = _median_time(config0, target_s / 3)
+    rows["config0"] = {"ms": round(1e3 * t0, 2), "runs": n0, "sampled": "no (whole call, L=216, to_qkv -> "
+                       "attention -> to_out)"}
+    # config 1: one full-length (batch, head) pair per run
     d, b = wl.DENSE_120S, wl.BAND_120S
-    # dense: one full-length (batch, head) pair at a time
     inp = wl.dense_inputs(1, d["length"], 1, d["head_dim"], seed=0, dtype="fp32")
     args = (inp["qkv"], inp["q_weight"], inp["k_weight"], inp["inv_freq"], inp["valid"], 1, d["head_dim"], 1e-6,
             inp["lam"], "fp32", np.float32)
-    odense.dense_xla(*args)  # warm
-    t0 = time.perf_counter()
-    n_dense = 0
-    while time.perf_counter() - t0 < target_s / 2 or n_dense < 2:
-        odense.dense_xla(*args)
-        n_dense += 1
-    dense_head_s = (time.perf_counter() - t0) / n_dense
-    dense_call_s = dense_head_s * d["batch"] * d["heads"]
-    # band: one head over a 16384-frame slice of the sequence
+    t1, n1 = _median_time(lambda: odense.dense_xla(*args), target_s / 3)
+    pairs = d["batch"] * d["heads"]
+    rows["config1_dense_call"] = {"ms": round(1e3 * t1 * pairs, 1), "runs": n1,
+                                  "sampled": f"1 of {pairs} (batch, head) pairs at L={d['length']}, x{pairs}"}
+    # config 2: one head over a 16384-frame slice per run
     frames = 16384
     binp = wl.band_inputs(1, frames, 1, b["head_dim"], b["window"], seed=1, dtype="fp32")
     bargs = (binp["qkv"], binp["q_norm"], binp["k_norm"], binp["inv_freq"], 1, b["head_dim"], b["window"], binp["lam"],
              "fp32", np.float32)
-    oband.band_xla(*bargs)
-    t0 = time.perf_counter()
-    n_band = 0
-    while time.perf_counter() - t0 < target_s / 2 or n_band < 2:
-        oband.band_xla(*bargs)
-        n_band += 1
-    band_slice_s = (time.perf_counter() - t0) / n_band
-    band_call_s = band_slice_s * (b["length"] / frames) * b["batch"] * b["heads"]
+    t2, n2 = _median_time(lambda: oband.band_xla(*bargs), target_s / 3)
+    scale = (b["length"] / frames) * b["batch"] * b["heads"]
+    rows["config2_band_call"] = {"ms": round(1e3 * t2 * scale, 1), "runs": n2,
+                                 "sampled": f"1 of {b['heads']} heads over {frames} of {b['length']} frames, "
+                                            f"x{scale:.2f}"}
     threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
-    ms_clip = 1e3 * (wl.DENSE_CALLS_PER_CLIP * dense_call_s + wl.BAND_CALLS_PER_CLIP * band_call_s)
+    ms_clip = (wl.DENSE_CALLS_PER_CLIP * rows["config1_dense_call"]["ms"]
+               + wl.BAND_CALLS_PER_CLIP * rows["config2_band_call"]["ms"])
     return {"value": round(ms_clip, 1), "unit": "ms/120s-clip", "cores": int(threads), "kind": "port",
-            "sample": (f"oracle (NumPy fp32 XLA-chain restatement): dense 1 of {d['batch'] * d['heads']} (batch, head) "
-                       f"pairs at L={d['length']} x{n_dense}, {dense_call_s * 1e3:.0f} ms/call scaled; band 1 of "
-                       f"{b['heads']} heads over {frames} of {b['length']} frames x{n_band}, "
-                       f"{band_call_s * 1e3:.0f} ms/call scaled; host cpus={len(os.sched_getaffinity(0))}")}
+            "sample": (f"oracle (NumPy fp32 XLA-chain restatement, not XLA: jax is absent), medians of >= 5 runs; "
+                       f"clip = {wl.DENSE_CALLS_PER_CLIP} config-1 dense calls + {wl.BAND_CALLS_PER_CLIP} config-2 band "
+                       f"calls, each scaled from its sample; host cpus={len(os.sched_getaffinity(0))}"),
+            "rows": rows}
 
 
 def call_percentiles(fn, n: int, stream) -> dict:
