@@ -244,6 +244,38 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
                          "ms_per_clip": round(wl.DENSE_CALLS_PER_CLIP * pc["p50"] / 1e3, 3)}
     del q, kv, ws, out
     res["same_l_block_120s"] = block_shape(lib, sp, stream, dev, gen)
+    res["dit_self_attention_120s"] = dit_self_attention_shape(stream, dev, gen)
+    return res
+
+
+def dit_self_attention_shape(stream, dev, gen) -> dict:
+    """One DiT self-attention (to_qkv -> differential attention -> to_out) at the 120 s clip (B=2, L=2584, width 1536
+    = 24 heads of 64, rotary half 16, bf16), with the projections on hipBLASLt ("torch": GEMM, then the kernel's own
+    key preparation) and on this package's GEMMs ("hip": key preparation in the to_qkv epilogue), per call."""
+    import dataclasses
+
+    import torch
+
+    from hummingbird_amd import dit
+    from hummingbird_amd import workloads as wl
+    from hummingbird_amd.config import MEDIUM_DIT
+
+    d = wl.DENSE_120S
+    cfg = dataclasses.replace(MEDIUM_DIT, num_memory_tokens=0)
+    B, L, E, H = d["batch"], d["length"], cfg.embed_dim, cfg.num_heads
+    h = torch.randn((B, L, E), device=dev, generator=gen).to(torch.bfloat16)
+
+    def w(o, i):
+        return (torch.randn((o, i), device=dev, generator=gen) / i ** 0.5).to(torch.bfloat16)
+    block = {"self_attn": {"to_qkv": {"weight": w(5 * E, E)}, "to_out": {"weight": w(E, E)},
+                           "q_norm": {"weight": torch.ones(64, device=dev)},
+                           "k_norm": {"weight": torch.ones(64, device=dev)}}}
+    static = dit.static_tables(torch.from_numpy(wl.inv_freq(cfg.rope_dim // 2)).to(dev),
+                               torch.ones((B, L), dtype=torch.bool, device=dev), cfg, torch.bfloat16)
+    res = {"shape": {"B": B, "L": L, "E": E, "H": H, "D": 64, "half": cfg.rope_dim // 2}}
+    for proj in ("torch", "hip"):
+        res[f"{proj}_us_per_call"] = call_percentiles(
+            lambda: dit.self_attention(h, block, static, cfg, projections=proj), 10, stream)
     return res
 
 

@@ -93,6 +93,21 @@ __device__ __forceinline__ f32x16 mfma_bf16_32x32x16(u32x4 a, u32x4 b, f32x16 c)
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                  0, 0, 0);
 }
+__device__ __forceinline__ f32x16 mfma_f16_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+// The 32x32x16 product of 16-bit operands stored in the IO type's own format (bf16 or half), fp32 accumulation.
+template <class IO>
+__device__ __forceinline__ f32x16 mfma_io_32x32x16(u32x4 a, u32x4 b, f32x16 c);
+template <>
+__device__ __forceinline__ f32x16 mfma_io_32x32x16<Bf16Io>(u32x4 a, u32x4 b, f32x16 c) {
+  return mfma_bf16_32x32x16(a, b, c);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma_io_32x32x16<F16Io>(u32x4 a, u32x4 b, f32x16 c) {
+  return mfma_f16_32x32x16(a, b, c);
+}
 __device__ __forceinline__ f32x16 mfma_f32_32x32x2(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }

@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 
 from hummingbird_amd import cross_attention as xattn
-from hummingbird_amd import dense_attention, xla_chain
+from hummingbird_amd import dense_attention, projection, xla_chain
 from hummingbird_amd.config import DiTConfig
 from hummingbird_amd.dtypes import Dtype
 
@@ -46,14 +46,35 @@ def static_tables(inv_freq: torch.Tensor, valid: torch.Tensor, cfg: DiTConfig,
 
 
 def self_attention(h: torch.Tensor, block: dict, static: dict, cfg: DiTConfig,
-                   lam: torch.Tensor | None = None, dtype: Dtype | None = None) -> torch.Tensor:
+                   lam: torch.Tensor | None = None, dtype: Dtype | None = None,
+                   projections: str = "torch") -> torch.Tensor:
     """`to_qkv` -> differential self-attention -> `to_out` (reference: dit._self_attention, dit.py:185-200).
     `block["self_attn"]` holds `to_qkv.weight (5E, E)`, `to_out.weight (E, E)`, `q_norm.weight`, `k_norm.weight`.
     `dtype` (a preset of hummingbird_amd.dtypes, as the reference's `dtype` argument) casts `h` and the projection
-    weights to its compute dtype; without it they are used as given."""
+    weights to its compute dtype; without it they are used as given.
+
+    `projections` picks the GEMMs around the HIP kernel: "torch" (hipBLASLt, then the kernel's own key
+    preparation) or "hip" (this package's matrix-core GEMMs with the key preparation in the to_qkv epilogue, so
+    `qkv` is never stored; bf16 or fp16, head_dim 64, heads a multiple of 4). Both compute the same cast points; the
+    choice only affects speed."""
     attn = block["self_attn"]
     if dtype is not None:
         h = h.to(dtype.compute)
+    half = cfg.rope_dim // 2
+    if projections not in ("torch", "hip"):
+        raise ValueError(f'projections must be "torch" or "hip", got {projections!r}')
+    if (projections == "hip" and use_hip(cfg, h)
+            and projection.fused_supported(h.dtype, cfg.num_heads, cfg.head_dim, h.shape[-1], half)):
+        qq, ws = projection.qkv_projection(h, attn["to_qkv"]["weight"], attn["k_norm"]["weight"], static["hip_cos"],
+                                           static["hip_sin"], static["hip_mask"], cfg.num_heads, cfg.head_dim, half,
+                                           cfg.qk_norm_eps)
+        out = projection.attend_projected(qq, attn["q_norm"]["weight"], attn["k_norm"]["weight"], static["hip_cos"],
+                                          static["hip_sin"], cfg.num_heads, cfg.head_dim, half, cfg.qk_norm_eps, ws,
+                                          lam=lam)
+        w_out = attn["to_out"]["weight"]
+        if projection.linear_supported(out.dtype, *w_out.shape):
+            return projection.linear(out, w_out)
+        return out @ w_out.to(out.dtype).t()
     qkv = h @ attn["to_qkv"]["weight"].to(h.dtype).t()
     if use_hip(cfg, qkv):
         out = dense_attention.dense_attention(qkv, attn["q_norm"]["weight"], attn["k_norm"]["weight"],

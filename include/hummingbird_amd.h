@@ -11,6 +11,9 @@
  *   hb_cross_attend              (sa3jax/dit.py:203-215, 274-284), which the reference runs without a kernel;
  *   hb_dyt, hb_glu     replace   the elementwise steps of same_l._block around its GEMMs (sa3jax/same_l.py:58-69,
  *                                172-192), an XLA chain in the reference;
+ *   hb_dit_qkv_proj,   replace   the GEMMs either side of the DiT kernel (sa3jax/dit.py:190, 195), the first with the
+ *   hb_dense_attend_qq,          dense kernel's key preparation in its epilogue;
+ *   hb_proj
  *   hb_rope_tables     replaces  band_attention.rope_tables / dit._rope_tables
  *                      (sa3jax/band_attention.py:43-58, sa3jax/dit.py:82-87) in a kernel-native layout.
  *
@@ -123,6 +126,30 @@ int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, int64_t row_
                     const float* q_weight, const float* k_weight, const float* cos, const float* sin, int half,
                     const float* lam, void* out, int B, int L, int H, int D, float eps,
                     const void* workspace, size_t workspace_bytes);
+
+/* ---- DiT self-attention projections ---------------------------------------------------------------------
+ * hb_dit_qkv_proj replaces `qkv = _linear(h, to_qkv)` (sa3jax/dit.py:190) together with the key-side half of
+ * dense_attention.dense_attention (the preparation of sa3jax/dense_attention.py:61-77): one matrix-core GEMM
+ * h (B*L, E) x W_qkv^T (E, 5*H*D) whose fp32 accumulators are rounded to the compute dtype (the reference's `qkv`)
+ * and then finished by section [q | k | v | q_diff | k_diff] (sa3jax/dit.py:196-198): q and q_diff are written to
+ * `qq` (B, L, 2*H*D) as rows [q | q_diff]; k and k_diff are RMS-normed with k_weight and rotated, v is multiplied
+ * by vmask, and all three are written to `workspace` in the layout hb_dense_prep produces. `qkv` itself is never
+ * stored. hb_dense_attend_qq then runs the attention of hb_dense_attend with its queries read from `qq`.
+ *   h      : (B, L, E) rows with stride h_row_stride (>= E, a multiple of 8), 16-byte aligned
+ *   w_qkv  : (5*H*D, E) row-major with stride w_row_stride (the layer's weight as stored, out x in)
+ *   dtype  : HB_BF16 or HB_F16;  D = 64;  H a multiple of 4;  E a multiple of 64;  half a multiple of 8 <= 32
+ *   cos, sin, vmask, k_weight, eps, workspace: as hb_dense_diffattn (workspace >= hb_dense_workspace_size)
+ * hb_proj replaces `_linear(x, W)` without bias (sa3jax/dit.py:195, the to_out projection): out (N, F) = x (N, K)
+ * x W^T (K, F) on the matrix cores, fp32 accumulation, one rounding to dtype; K a multiple of 64, F of 256. */
+int hb_dit_qkv_proj(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* w_qkv,
+                    int64_t w_row_stride, int E, const float* k_weight, const float* cos, const float* sin, int half,
+                    const float* vmask, void* qq, int B, int L, int H, int D, float eps, void* workspace,
+                    size_t workspace_bytes);
+int hb_dense_attend_qq(hipStream_t stream, const void* qq, int dtype, int64_t row_stride, const float* q_weight,
+                       const float* k_weight, const float* cos, const float* sin, int half, const float* lam, void* out,
+                       int B, int L, int H, int D, float eps, const void* workspace, size_t workspace_bytes);
+int hb_proj(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const void* w, int64_t w_row_stride,
+            void* out, int64_t out_row_stride, int64_t N, int K, int F);
 
 /* ---- SAME-L band differential attention -----------------------------------------------------------------
  * Replaces band_attention.band_attention (sa3jax/band_attention.py:123-180) and the XLA chain it stands in

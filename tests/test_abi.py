@@ -146,3 +146,35 @@ def test_noalloc_rejects_before_touching_the_gpu(lib):
     assert b"no-allocation" in lib.hb_last_error()
     assert call(100, D=96) == 4  # HB_ERR_HEAD_DIM
     assert call(100, qkv=None) == 1  # HB_ERR_NULL
+
+
+def test_projection_entry_points_reject_before_any_launch(lib):
+    """hb_dit_qkv_proj, hb_dense_attend_qq and hb_proj validate dtype, shapes, strides, alignment and the workspace
+    on the host (no kernel is launched here)."""
+    fake = 0x100000
+    B, L, H, D, E = 2, 100, 4, 64, 256
+    need = lib.hb_dense_workspace_size(0, B, L, H, D)
+
+    def qkv(**kw):
+        a = dict(h=fake, dtype=0, hs=E, w=fake, wstride=E, E=E, kw=fake, cos=fake, sin=fake, half=32, qq=fake, B=B,
+                 L=L, H=H, D=D, eps=1e-6, ws=fake, wsb=need)
+        a.update(kw)
+        return lib.hb_dit_qkv_proj(None, a["h"], a["dtype"], a["hs"], a["w"], a["wstride"], a["E"], a["kw"], a["cos"],
+                                   a["sin"], a["half"], None, a["qq"], a["B"], a["L"], a["H"], a["D"], a["eps"],
+                                   a["ws"], a["wsb"])
+    assert qkv(dtype=1) == 3            # fp32 is not taken by the fused projection
+    assert qkv(D=128) == 4
+    assert qkv(H=6) == 2                # heads must be a multiple of 4
+    assert qkv(E=100) == 2              # model width a multiple of 64
+    assert qkv(half=40) == 5
+    assert qkv(hs=E - 8) == 7           # row stride below the width
+    assert qkv(h=fake + 8) == 7         # misaligned input
+    assert qkv(wsb=need - 1) == 8
+    assert qkv(h=None) == 1
+    proj = lambda **kw: lib.hb_proj(None, kw.get("x", fake), kw.get("dtype", 0), kw.get("xs", 128), fake,  # noqa: E731
+                                    128, fake, kw.get("os", 256), kw.get("N", 10), kw.get("K", 128), kw.get("F", 256))
+    assert proj(F=200) == 2 and proj(K=100) == 2 and proj(N=0) == 2 and proj(dtype=1) == 3 and proj(os=100) == 7
+    attend = lambda **kw: lib.hb_dense_attend_qq(None, fake, kw.get("dtype", 0), kw.get("rs", 2 * H * D), fake,  # noqa: E731
+                                                 fake, fake, fake, 32, None, fake, B, L, H, D, 1e-6,
+                                                 kw.get("ws", fake), kw.get("wsb", need))
+    assert attend(rs=2 * H * D - 8) == 7 and attend(dtype=1) == 3 and attend(wsb=need - 1) == 8

@@ -41,6 +41,29 @@ def test_dit_self_attention_hip_vs_xla(dtype):
     check(got.float().cpu().numpy(), ref.float().cpu().numpy(), f"dit {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_dit_self_attention_hip_projections_vs_xla(dtype):
+    """projections="hip" (the fused to_qkv GEMM + attention over its output + the to_out GEMM) against the XLA
+    chain on the same weights, and against projections="torch" at the bf16 contract."""
+    from hummingbird_amd import projection
+
+    print(f"\n[case] dit.self_attention hip projections {dtype}", flush=True)
+    cfg = MEDIUM_DIT
+    assert projection.fused_supported(dtype, cfg.num_heads, cfg.head_dim, cfg.embed_dim, cfg.rope_dim // 2)
+    h, valid, inv_freq, block, lam = dit_case(cfg, 2, 216 - cfg.num_memory_tokens)
+    h, block = to(h, dtype), to(block, dtype)
+    for norm in ("q_norm", "k_norm"):
+        block["self_attn"][norm]["weight"] = block["self_attn"][norm]["weight"].float()
+    inv_freq, valid, lam = inv_freq.to(DEV), valid.to(DEV), lam.to(DEV)
+    static = dit.static_tables(inv_freq, valid, cfg, dtype)
+    got = dit.self_attention(h, block, static, cfg, lam=lam, projections="hip")
+    unfused = dit.self_attention(h, block, static, cfg, lam=lam, projections="torch")
+    xcfg = dataclasses.replace(cfg, attention="xla")
+    ref = dit.self_attention(h, block, dit.static_tables(inv_freq, valid, xcfg, dtype), xcfg, lam=lam)
+    assert_bf16_parity(got.float().cpu().numpy(), unfused.float().cpu().numpy(), f"hip vs torch projections {dtype}")
+    assert_bf16_parity(got.float().cpu().numpy(), ref.float().cpu().numpy(), f"hip projections vs xla {dtype}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
 def test_same_l_attention_hip_vs_xla(dtype):
     print(f"\n[case] same_l.attention hip vs xla {dtype}", flush=True)
