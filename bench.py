@@ -55,6 +55,9 @@ def parse() -> argparse.Namespace:
                          "GEMMs (8192^3) and the dense call with N(0,1), all-zero and all-one inputs")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the per-call timings at the reference-true and 380 s shapes")
+    ap.add_argument("--sampler-only", action="store_true",
+                    help="instead of the clip benchmark: the whole 120 s render of the medium DiT (8 pingpong steps "
+                         "x 24 blocks, eager and as one HIP graph), one JSON line; for profiling under rocprofv3")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel timing loops plus one 256 MiB device copy (the traffic-counter "
                          "calibration kernel); for profiling under rocprofv3")
@@ -245,7 +248,52 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
     del q, kv, ws, out
     res["same_l_block_120s"] = block_shape(lib, sp, stream, dev, gen)
     res["dit_self_attention_120s"] = dit_self_attention_shape(stream, dev, gen)
+    res["sampler_120s"] = sampler_shape(dev)
     return res
+
+
+def sampler_shape(dev) -> dict:
+    """The whole denoising of one 120 s clip as the reference renders it: the `medium` DiT (24 blocks, width 1536,
+    24 heads; random weights), batch 1, 1358 latents + 64 memory tokens (L = 1422), a 257-token context, 8 pingpong
+    steps, bf16, attention="hip" (192 dense self-attention and 192 cross-attention calls). Per-clip state from
+    `dit.prepare_static` (not timed); then ms per clip for the eager loop and for the loop captured as one HIP
+    graph (median of 3 each)."""
+    import torch
+
+    from hummingbird_amd import dit, sampling
+    from hummingbird_amd.config import MEDIUM_DIT, SAMPLER_STEPS
+    from hummingbird_amd.dtypes import BF16
+
+    cfg, T, steps = MEDIUM_DIT, 1358, SAMPLER_STEPS
+    gen = torch.Generator(device=dev).manual_seed(11)
+    params = dit.init_params(cfg, BF16, device=dev, seed=11)
+    cond = {"cross_attn_cond": torch.randn((1, 257, cfg.cond_token_dim), device=dev, generator=gen),
+            "global_cond": torch.randn((1, cfg.global_cond_dim), device=dev, generator=gen)}
+    mask = torch.ones((1, T), dtype=torch.bool, device=dev)
+    x0 = torch.randn((1, cfg.io_channels, T), device=dev, generator=gen)
+    noise = torch.zeros((steps, 1, cfg.io_channels, T), device=dev)  # the "zeros" renoise the ports ship
+    static = dit.prepare_static(params, cond, mask, cfg, BF16)
+    schedule = sampling.build_schedule(steps, device=dev)
+
+    def clip_ms(fn, n=3) -> float:
+        fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(n):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b))
+        return round(float(np.median(times)), 2)
+    eager = clip_ms(lambda: sampling.pingpong(params, x0, schedule, noise, static, cfg, BF16, trajectory=False))
+    graph = sampling.PingpongGraph(params, static, cfg, BF16, x0, noise)
+    replay = clip_ms(lambda: graph(x0, noise))
+    return {"shape": {"B": 1, "latents": T, "L": T + cfg.num_memory_tokens, "context": 257, "depth": cfg.depth,
+                      "E": cfg.embed_dim, "H": cfg.num_heads, "steps": steps},
+            "eager_ms_per_clip": eager, "graph_ms_per_clip": replay,
+            "attention_calls_per_clip": {"dense": steps * cfg.depth, "cross": steps * cfg.depth}}
 
 
 def dit_self_attention_shape(stream, dev, gen) -> dict:
@@ -481,6 +529,9 @@ def main() -> int:
         return 0
     if args.ceiling:
         ceiling(lib, sp, stream, dev)
+        return 0
+    if args.sampler_only:
+        print(json.dumps({"sampler_120s": sampler_shape(dev)}), flush=True)
         return 0
 
     # ---- dense inputs (two qkv buffers alternate, as consecutive blocks would) ----

@@ -1,5 +1,6 @@
-"""Hot-path configuration: the reference's DiTConfig / SameConfig fields the two attention kernels read
-(sa3jax/config.py:36-78, 81-141), with `"hip"` added to both `attention` literals.
+"""Configuration: the reference's DiTConfig (sa3jax/config.py:36-78) and the SameConfig fields the band kernel
+reads (sa3jax/config.py:81-141), with `"hip"` added to both `attention` literals; the sampler's constants
+(sa3jax/config.py:158-165, sa3jax/pipeline.py:43-45).
 
 `attention="hip"` selects the MI355X kernels (`dense_attention` / `band_attention` of this package). The other
 values keep the reference's meaning: `"xla"` is the plain chain (here restated in torch, any device), and
@@ -14,14 +15,24 @@ from typing import Literal
 
 @dataclass(frozen=True)
 class DiTConfig:
-    """DiT self-attention fields (sa3jax/config.py:36-78)."""
+    """The DiT's fields (sa3jax/config.py:36-78): the self-attention geometry the kernels read, and the model
+    fields `dit.dit_forward` and the sampler read (channels, depth, conditioning widths, feed-forward width,
+    norm eps, timestep features)."""
 
+    io_channels: int = 256
     embed_dim: int = 1024
+    depth: int = 20
     num_heads: int = 16
+    cond_token_dim: int = 768
+    global_cond_dim: int = 768
+    local_add_cond_dim: int = 257
+    num_memory_tokens: int = 64
+    ff_mult: float = 4.0
     differential: bool = False
+    norm_eps: float = 1e-5
     qk_norm_eps: float = 1e-6
     rope_theta: float = 10000.0
-    num_memory_tokens: int = 64
+    fourier_dim: int = 256
     attention: Literal["xla", "fused", "hip"] = "xla"
     fused_min_tokens: int = 800  # the TPU kernel's floor; the "hip" kernel has none
 
@@ -33,6 +44,15 @@ class DiTConfig:
     def rope_dim(self) -> int:
         """`RotaryEmbedding(max(head_dim // 2, 32))`: partial rotary (sa3jax/config.py:67-70)."""
         return max(self.head_dim // 2, 32)
+
+    @property
+    def ff_inner(self) -> int:
+        return int(self.embed_dim * self.ff_mult)
+
+    @property
+    def adaln_dim(self) -> int:
+        """Scale, shift and gate of the self-attention and the feed-forward: 6 * embed_dim."""
+        return 6 * self.embed_dim
 
 
 @dataclass(frozen=True)
@@ -75,6 +95,12 @@ class SameConfig:
 
 
 # The `medium` preset's attention geometry (sa3jax/config.py:171-185) with the MI355X kernels selected.
-MEDIUM_DIT = DiTConfig(embed_dim=1536, num_heads=24, differential=True, attention="hip")
+MEDIUM_DIT = DiTConfig(embed_dim=1536, depth=24, num_heads=24, differential=True, attention="hip")
 MEDIUM_SAME_L = SameConfig(channels=256, transformer_depth=12, sliding_window=(1, 1), sinusoidal_blocks=8,
                            attention="hip")
+
+# The sampler (sa3jax/config.py:163-164; the LogSNR shift of sa3jax/pipeline.py:43-45).
+SAMPLER_STEPS = 8
+SIGMA_MAX = 1.0
+ANCHOR_LOGSNR = -6.2
+LOGSNR_END = 2.0

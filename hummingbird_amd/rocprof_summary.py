@@ -39,15 +39,31 @@ def short_name(name: str) -> str:
         if args and args[0] in IO_SUFFIX:
             base, args = base + IO_SUFFIX[args[0]], args[1:]
         return base + (f"<{','.join(args)}>" if args else "")
+    if "at::native::" in name:  # torch: the kernel template and the operation it applies
+        head = re.search(r"at::native::(?:\(anonymous namespace\)::)?(\w+)", name)
+        ops = re.findall(r"(\w+(?:Functor\w*|_kernel_cuda|Ops|_copy_kernel_cuda))", name[head.end():] if head else name)
+        kinds = re.findall(r"c10::(BFloat16|Half)|<(float|double)", name)
+        elem = next((a or b for a, b in kinds), "")
+        label = head.group(1) if head else "torch"
+        return f"torch {label}<{ops[0] if ops else ''}{', ' + elem if elem else ''}>"
     return name.split("(")[0][:60]
 
 
 def kernel_stats(trace_dir: Path) -> dict[str, dict]:
-    rows = {}
+    """Per short name: calls, average / min / max duration and share of GPU time, summed over the kernels that
+    share the short name."""
+    rows: dict[str, dict] = {}
     for r in csv.DictReader(open(trace_dir / "run_kernel_stats.csv")):
-        rows[short_name(r["Name"])] = {"calls": int(r["Calls"]), "avg_us": float(r["AverageNs"]) / 1e3,
-                                       "min_us": float(r["MinNs"]) / 1e3, "max_us": float(r["MaxNs"]) / 1e3,
-                                       "pct": float(r["Percentage"])}
+        k, calls = short_name(r["Name"]), int(r["Calls"])
+        total = float(r["TotalDurationNs"]) / 1e3 if r.get("TotalDurationNs") else calls * float(r["AverageNs"]) / 1e3
+        e = rows.setdefault(k, {"calls": 0, "total_us": 0.0, "min_us": float("inf"), "max_us": 0.0, "pct": 0.0})
+        e["calls"] += calls
+        e["total_us"] += total
+        e["min_us"] = min(e["min_us"], float(r["MinNs"]) / 1e3)
+        e["max_us"] = max(e["max_us"], float(r["MaxNs"]) / 1e3)
+        e["pct"] += float(r["Percentage"])
+    for e in rows.values():
+        e["avg_us"] = e["total_us"] / max(e["calls"], 1)
     return rows
 
 

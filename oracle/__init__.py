@@ -12,6 +12,9 @@ This package restates, in NumPy, the arithmetic of the reference's XLA attention
   attentions over the context, subtract (sa3jax/dit.py:203-215, 274-284, 131-176), built from `oracle.dense`.
 * `oracle.block` -- the SAME-L decoder block (sa3jax/same_l.py:58-69, 151-192): DyT, to_qkv, band attention,
   to_out, residual; DyT, glu_proj, the GLU gate, proj_out, residual; built from `oracle.band`.
+* `oracle.dit` -- the DiT denoiser around the self- and cross-attention (sa3jax/dit.py:31-79, 218-361) and the
+  pingpong sampler with its LogSNR-shift schedule (sa3jax/sampling.py:65-118), built from `oracle.dense` and
+  `oracle.cross`.
 * `oracle.bf16` -- round-to-nearest-even bfloat16 emulation for the cast points.
 
 Only `tests/`, `__graft_entry__.smoke()` and `bench.py`'s CPU-baseline leg may import this package,
@@ -40,9 +43,17 @@ How each function is pinned (the checks live in tests/test_oracle.py):
   a known case; the block with both branches off is the identity; the FF branch alone against a torch float64
   composition; the attention branch alone against torch's SDPA under an explicit band mask.
 
+* DiT denoiser and sampler (tests/test_sampler.py): the schedule against the values the reference documents for
+  the shipped sampler (t[1] is 0.99609375 in bf16 and 0.994140625 in half) and its special cases; the pingpong
+  step against closed forms with stub denoisers; the timestep features at their end-point frequencies; the 1x1
+  convolution against a brute-force sum; the depth-0 denoiser against its linear maps composed in float64; the
+  adaLN block on known cases (cancelling branches give the identity, the local constant on the latent tokens
+  only, the sigmoid(1 - gate) gate, the x (1 + scale) + shift modulation through an exactly-identity
+  feed-forward).
+
 Parity unpinned: the bit-level behaviour of XLA itself (where it rounds einsum outputs, its exp/cos/sin/tanh
 ulps and reduction order) cannot be pinned here because jax is not installed; the oracle fixes the cast
 points the reference's source states, and the tolerance contract (bf16: max-abs <= 2e-2 and cosine >=
 0.9999; fp32: <= 1e-5 relative) absorbs the remaining ulp-level differences.
 """
-from oracle import band, bf16, block, cross, dense  # noqa: F401
+from oracle import band, bf16, block, cross, dense, dit  # noqa: F401
