@@ -19,7 +19,7 @@ BUILD = PKG / "_build"
 LIB = PKG / "libhummingbird_amd.so"
 ARCH = "gfx950"
 SOURCES = ("api.cpp", "cross.cpp", "dense.hip", "band.hip", "band_ring.hip", "band_tiled.hip", "fp32.hip", "elementwise.hip",
-           "proj.hip")
+           "proj.hip", "dit_block.hip")
 
 # Device flags. Packed fp32 instructions are disabled for every HIP source: hipcc -O3 would otherwise form
 # v_pk_{add,mul,fma}_f32 from ordinary float code. Floating-point contraction is off so that separately

@@ -73,18 +73,20 @@ __device__ __forceinline__ SoftmaxPlan softmax_plan(float qn, float kn, int D) {
 // 16 kk + 8 lh .. +8. `vf(dt, g)` is the A operand of O^T: dim 32 dt + lr of the eight keys
 // {16 g + 8 (j / 4) + 4 lh + j % 4 : j < 8} that the lane's probability registers hold (see v_frag).
 // `qf(b, ct, kk)` is the B operand (8 bf16 of this lane's query in column tile ct) for branch slot b and dims
-// 16 kk + 8 lh .. +8.
-template <int D, int NB, int NCT, bool FAST, class KFrag, class VFrag, class QFrag, class Valid>
+// 16 kk + 8 lh .. +8. RT: 32-key row tiles attended (2 = the whole tile; 1 = its first 32 keys only, for a last
+// tile whose other keys do not exist: their probabilities would be 0 and their products add nothing).
+template <int D, int NB, int NCT, bool FAST, int RT = 2, class KFrag, class VFrag, class QFrag, class Valid>
 __device__ __forceinline__ void attend_tile(KFrag kf, VFrag vf, QFrag qf, f32x16 (&o)[NB][NCT][D / 32],
                                             float (&lsum)[NB][NCT], float (&m)[NB][NCT], float c, bool masked,
                                             Valid valid) {
+  static_assert(RT == 1 || RT == 2, "a tile is one or two 32-key row tiles");
   const int lane = threadIdx.x & 63, lh = lane >> 5;
   u32x4 pb[NB][NCT][2][2];  // [branch][column tile][row tile][16-key half]: 8 bf16 probabilities each
 #pragma unroll
   for (int br = 0; br < NB; ++br) {
     f32x16 sc[NCT][2];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       f32x16 acc[NCT];
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) acc[ct] = f32x16{};
@@ -101,7 +103,7 @@ __device__ __forceinline__ void attend_tile(KFrag kf, VFrag vf, QFrag qf, f32x16
     for (int ct = 0; ct < NCT; ++ct) {
       if (masked) {
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
             sc[ct][rt][r] = valid(acc_key(rt, r, lh), ct) ? sc[ct][rt][r] : -INFINITY;
@@ -110,7 +112,7 @@ __device__ __forceinline__ void attend_tile(KFrag kf, VFrag vf, QFrag qf, f32x16
       if constexpr (!FAST) {
         float mt = -INFINITY;
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[ct][rt][r]);
         mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * c;
@@ -124,7 +126,7 @@ __device__ __forceinline__ void attend_tile(KFrag kf, VFrag vf, QFrag qf, f32x16
         mb = mn == -INFINITY ? 0.f : mn;
       }
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -147,7 +149,7 @@ __device__ __forceinline__ void attend_tile(KFrag kf, VFrag vf, QFrag qf, f32x16
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
+    for (int g = 0; g < 2 * RT; ++g) {
       const u32x4 a = vf(dt, g);
 #pragma unroll
       for (int br = 0; br < NB; ++br)

@@ -20,6 +20,7 @@
 // softmax (running max with rescaling) with the reference fused kernel's cast points; the choice is uniform
 // for the whole launch (SoftmaxPlan in attn_tile.h).
 #include <mutex>
+#include <type_traits>
 
 #include "api.h"
 #include "attn_tile.h"
@@ -199,8 +200,8 @@ __device__ __forceinline__ void dense_attend_loop(
   // The next tile is copied into the other LDS stage while the current one is attended; one wait and one
   // barrier per tile.
   const int lr = tid & 31, lh = (tid >> 5) & 1;
-  auto attend = [&](const uint16_t* s, bool masked, int kt0) {
-    attend_tile<D, NB, NCT, FAST>(
+  auto attend = [&](const uint16_t* s, bool masked, int kt0, auto row_tiles) {
+    attend_tile<D, NB, NCT, FAST, decltype(row_tiles)::value>(
         [&](int b, int rt, int kk) { return lds16(s + (br0 + b) * T::K_ELEMS + swz<D>(32 * rt + lr, 2 * kk + lh)); },
         [&](int dt, int g) { return lds16(s + 2 * T::K_ELEMS + swz<64>(32 * dt + lr, 2 * g + lh)); },
         [&](int b, int ct, int kk) { return qf[b][ct][kk]; }, o, lsum, m, c, masked,
@@ -216,25 +217,34 @@ __device__ __forceinline__ void dense_attend_loop(
   const uint32_t ldsA = lds_addr(sA), ldsB = lds_addr(sB);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  const std::integral_constant<int, 2> whole;
+  const std::integral_constant<int, 1> first_half;
   int t = 0;
   for (; t + 1 < nfull; t += 2) {
     issue(t + 1, ldsB);  // stage B was last read in tile t - 1
-    attend(sA, false, 0);
+    attend(sA, false, 0, whole);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (t + 2 < nkt) issue(t + 2, ldsA);
-    attend(sB, false, 0);
+    attend(sB, false, 0, whole);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
   if (t < nfull) {  // an odd number of full tiles: the last one sits in stage A
     if (t + 1 < nkt) issue(t + 1, ldsB);
-    attend(sA, false, 0);
+    attend(sA, false, 0, whole);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     ++t;
   }
-  if (nfull < nkt) attend((nfull & 1) ? sB : sA, true, nfull * 64);  // the ragged last tile
+  if (nfull < nkt) {  // the ragged last tile; at D = 64 with at most 32 keys left only its first row tile is
+                      // attended (at D = 128 the extra inlined copy would spill registers)
+    const uint16_t* s = (nfull & 1) ? sB : sA;
+    if (D == 64 && L - nfull * 64 <= 32)
+      attend(s, true, nfull * 64, first_half);
+    else
+      attend(s, true, nfull * 64, whole);
+  }
 }
 
 // RMSNorm (dit.py:45-57), rotate-half RoPE over the first 2 * 8 H8 dims (dit.py:90-98) and the softmax scale of

@@ -1,0 +1,271 @@
+// The elementwise steps of a DiT block around its GEMMs and attention calls, for gfx950 (MI355X).
+//
+// Replaces the chain of dit._block between the matmuls (sa3jax/dit.py:224-251), which the reference leaves to
+// XLA as separate array operations:
+//   rms_modulate    x = rms(h) * (1 + scale) + shift: the block RMSNorm (dit.py:44-57; fp32 mean of squares,
+//                   the stored scale applied in fp32, cast back) followed by the adaLN modulation of the self-
+//                   attention or feed-forward input (dit.py:231-233, 246-247), or the plain norm (no scale and
+//                   shift) of the cross-attention input (dit.py:236);
+//   gated_residual  out = h + (x + bias) * sigmoid(1 - gate): the gated residuals of the self-attention and the
+//                   feed-forward (dit.py:234, 249-251; the bias is proj_out's, dit.py:221), or the plain residual
+//                   of the cross-attention (dit.py:237) followed by the constant local embedding on the latent
+//                   tokens (dit.py:239-241).
+// Each is one HBM pass over 16-byte chunks. bf16 and half round where the reference holds an array of the compute
+// dtype: after the norm, 1 + scale, the product, the shift; x + bias, 1 - gate, the sigmoid, the product, the
+// residual sum, the local sum. fp32 does not round.
+#include <cmath>
+
+#include "api.h"
+#include "common.h"
+
+namespace hb {
+namespace blk {
+
+template <typename T>
+struct Vec;
+template <>
+struct Vec<uint16_t> {  // bf16
+  static constexpr int N = 8;
+  __device__ static void load(const uint16_t* p, float (&x)[8]) { unpack8(ld16(p), x); }
+  __device__ static void store(uint16_t* p, const float (&x)[8]) { st16(p, pack8(x)); }
+  __device__ static float round(float x) { return round_bf16(x); }
+};
+template <>
+struct Vec<_Float16> {  // IEEE half
+  static constexpr int N = 8;
+  __device__ static void load(const _Float16* p, float (&x)[8]) { F16Io::unpack8(ld16(p), x); }
+  __device__ static void store(_Float16* p, const float (&x)[8]) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = F16Io::pack2(x[2 * i], x[2 * i + 1]);
+    st16(p, v);
+  }
+  __device__ static float round(float x) { return F16Io::round(x); }
+};
+template <>
+struct Vec<float> {  // fp32
+  static constexpr int N = 4;
+  __device__ static void load(const float* p, float (&x)[4]) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = v[i];
+  }
+  __device__ static void store(float* p, const float (&x)[4]) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+  }
+  __device__ static float round(float x) { return x; }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// One wave per row: the mean of squares over the row (fp32), then the normalised row scaled by `w` (fp32), cast,
+// and with `scale` the modulation by the row's batch entry of `scale` / `shift` (`mod_stride` elements apart per
+// batch, `L` rows per batch). The row is read twice; the second read hits the cache.
+template <typename T>
+__global__ __launch_bounds__(256) void rms_modulate_kernel(const T* __restrict__ x, int64_t xs,
+                                                           const float* __restrict__ w, float eps,
+                                                           const T* __restrict__ scale, const T* __restrict__ shift,
+                                                           int64_t mod_stride, int L, T* __restrict__ out, int64_t os,
+                                                           int64_t N, int C) {
+  constexpr int V = Vec<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + wave_id();
+  if (n >= N) return;  // wave-uniform
+  const T* row = x + n * xs;
+  float ss = 0.f;
+  for (int c0 = lane * V; c0 < C; c0 += 64 * V) {
+    float v[V];
+    Vec<T>::load(row + c0, v);
+#pragma unroll
+    for (int j = 0; j < V; ++j) ss = ss + v[j] * v[j];
+  }
+  const float inv = rsqrtf(wave_sum(ss) * (1.f / static_cast<float>(C)) + eps);
+  const int64_t b = n / L;
+  const T* sc = scale ? scale + b * mod_stride : nullptr;
+  const T* sh = shift ? shift + b * mod_stride : nullptr;
+  T* orow = out + n * os;
+  for (int c0 = lane * V; c0 < C; c0 += 64 * V) {
+    float v[V];
+    Vec<T>::load(row + c0, v);
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = Vec<T>::round((v[j] * inv) * w[c0 + j]);
+    if (sc) {
+      float s[V], t[V];
+      Vec<T>::load(sc + c0, s);
+      Vec<T>::load(sh + c0, t);
+#pragma unroll
+      for (int j = 0; j < V; ++j) v[j] = Vec<T>::round(Vec<T>::round(v[j] * Vec<T>::round(1.f + s[j])) + t[j]);
+    }
+    Vec<T>::store(orow + c0, v);
+  }
+}
+
+// Grid-stride walk over the (row, 16-byte chunk) pairs. Row n belongs to batch n / L at token n % L.
+template <typename T>
+__global__ __launch_bounds__(256) void gated_residual_kernel(const T* __restrict__ h, int64_t hs,
+                                                             const T* __restrict__ x, int64_t xs,
+                                                             const T* __restrict__ xbias, const T* __restrict__ gate,
+                                                             int64_t gate_stride, const T* __restrict__ local,
+                                                             int memory, int L, T* __restrict__ out, int64_t os,
+                                                             int64_t N, int C) {
+  constexpr int V = Vec<T>::N;
+  const int chunks = C / V;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < N * chunks;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t n = i / chunks;
+    const int c0 = static_cast<int>(i - n * chunks) * V;
+    float hv[V], xv[V];
+    Vec<T>::load(h + n * hs + c0, hv);
+    Vec<T>::load(x + n * xs + c0, xv);
+    if (xbias) {
+      float bv[V];
+      Vec<T>::load(xbias + c0, bv);
+#pragma unroll
+      for (int j = 0; j < V; ++j) xv[j] = Vec<T>::round(xv[j] + bv[j]);
+    }
+    if (gate) {
+      float g[V];
+      Vec<T>::load(gate + (n / L) * gate_stride + c0, g);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float u = Vec<T>::round(1.f - g[j]);
+        xv[j] = Vec<T>::round(xv[j] * Vec<T>::round(1.f / (1.f + expf(-u))));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) hv[j] = Vec<T>::round(hv[j] + xv[j]);
+    if (local && static_cast<int>(n % L) >= memory) {
+      float lv[V];
+      Vec<T>::load(local + c0, lv);
+#pragma unroll
+      for (int j = 0; j < V; ++j) hv[j] = Vec<T>::round(hv[j] + lv[j]);
+    }
+    Vec<T>::store(out + n * os + c0, hv);
+  }
+}
+
+}  // namespace blk
+}  // namespace hb
+
+using namespace hb;
+
+namespace {
+
+int vec_of(int dtype) { return dtype == HB_F32 ? 4 : 8; }
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+int check_common(const char* what, int dtype, int64_t N, int C, int L) {
+  if (dtype != HB_BF16 && dtype != HB_F32 && dtype != HB_F16)
+    return fail(HB_ERR_DTYPE, "dtype %d is not HB_BF16 (0), HB_F32 (1) or HB_F16 (2)", dtype);
+  if (N < 1 || C < 1 || N > (int64_t(1) << 31) || L < 1)
+    return fail(HB_ERR_SHAPE, "%s needs 1 <= N <= 2^31, C >= 1 and rows_per_batch >= 1", what);
+  if (C % vec_of(dtype)) return fail(HB_ERR_SHAPE, "%s needs C (%d) to be a multiple of %d", what, C, vec_of(dtype));
+  return HB_OK;
+}
+
+int check_tensor(const char* what, const char* name, const void* p, int64_t stride, int64_t min_stride, int dtype,
+                 bool required) {
+  if (!p) return required ? fail(HB_ERR_NULL, "%s: %s must be non-NULL", what, name) : HB_OK;
+  if (!aligned16(p)) return fail(HB_ERR_STRIDE, "%s: %s must be 16-byte aligned", what, name);
+  if (stride < min_stride || stride % vec_of(dtype))
+    return fail(HB_ERR_STRIDE, "%s: %s stride %lld must be >= %lld and a multiple of %d", what, name,
+                static_cast<long long>(stride), static_cast<long long>(min_stride), vec_of(dtype));
+  return HB_OK;
+}
+
+int launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(HB_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
+  return HB_OK;
+}
+
+template <typename T>
+void launch_rms(hipStream_t s, const void* x, int64_t xs, const float* w, float eps, const void* scale,
+                const void* shift, int64_t ms, int L, void* out, int64_t os, int64_t N, int C) {
+  const dim3 grid(static_cast<unsigned>((N + 3) / 4));
+  hipLaunchKernelGGL(blk::rms_modulate_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x), xs, w, eps,
+                     static_cast<const T*>(scale), static_cast<const T*>(shift), ms, L, static_cast<T*>(out), os, N,
+                     C);
+}
+
+template <typename T>
+void launch_residual(hipStream_t s, const void* h, int64_t hs, const void* x, int64_t xs, const void* xbias,
+                     const void* gate, int64_t gs, const void* local, int memory, int L, void* out, int64_t os,
+                     int64_t N, int C) {
+  const int64_t chunks = C / blk::Vec<T>::N;
+  const int64_t need = (N * chunks + 255) / 256, cap = 16 * static_cast<int64_t>(device_cus());
+  hipLaunchKernelGGL(blk::gated_residual_kernel<T>, dim3(static_cast<unsigned>(need < cap ? need : cap)), dim3(256),
+                     0, s, static_cast<const T*>(h), hs, static_cast<const T*>(x), xs, static_cast<const T*>(xbias),
+                     static_cast<const T*>(gate), gs, static_cast<const T*>(local), memory, L, static_cast<T*>(out), os,
+                     N, C);
+}
+
+}  // namespace
+
+extern "C" {
+
+int hb_rms_modulate(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const float* weight,
+                    float eps, const void* scale, const void* shift, int64_t mod_batch_stride, int rows_per_batch,
+                    void* out, int64_t out_row_stride, int64_t N, int C) {
+  clear_error();
+  int st = check_common("rms_modulate", dtype, N, C, rows_per_batch);
+  if (st) return st;
+  if ((st = check_tensor("rms_modulate", "x", x, x_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("rms_modulate", "out", out, out_row_stride, C, dtype, true))) return st;
+  if (!weight) return fail(HB_ERR_NULL, "rms_modulate: weight must be non-NULL");
+  if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(HB_ERR_EPS, "rms_modulate: eps %g must be finite and >= 0", eps);
+  if (!scale != !shift) return fail(HB_ERR_NULL, "rms_modulate: scale and shift are given together or not at all");
+  if (scale) {
+    if (N % rows_per_batch) return fail(HB_ERR_SHAPE, "rms_modulate: N must be a multiple of rows_per_batch");
+    const int64_t stride = N / rows_per_batch > 1 ? mod_batch_stride : C;  // unused with a single batch
+    if ((st = check_tensor("rms_modulate", "scale", scale, stride, C, dtype, true))) return st;
+    if ((st = check_tensor("rms_modulate", "shift", shift, stride, C, dtype, true))) return st;
+  }
+  if (dtype == HB_BF16)
+    launch_rms<uint16_t>(stream, x, x_row_stride, weight, eps, scale, shift, mod_batch_stride, rows_per_batch, out,
+                         out_row_stride, N, C);
+  else if (dtype == HB_F16)
+    launch_rms<_Float16>(stream, x, x_row_stride, weight, eps, scale, shift, mod_batch_stride, rows_per_batch, out,
+                         out_row_stride, N, C);
+  else
+    launch_rms<float>(stream, x, x_row_stride, weight, eps, scale, shift, mod_batch_stride, rows_per_batch, out,
+                      out_row_stride, N, C);
+  return launched("rms_modulate");
+}
+
+int hb_gated_residual(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* x,
+                      int64_t x_row_stride, const void* x_bias, const void* gate, int64_t gate_batch_stride,
+                      const void* local, int memory, int rows_per_batch, void* out, int64_t out_row_stride,
+                      int64_t N, int C) {
+  clear_error();
+  int st = check_common("gated_residual", dtype, N, C, rows_per_batch);
+  if (st) return st;
+  if ((st = check_tensor("gated_residual", "h", h, h_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("gated_residual", "x", x, x_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("gated_residual", "out", out, out_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("gated_residual", "x_bias", x_bias, C, C, dtype, false))) return st;
+  if ((st = check_tensor("gated_residual", "local", local, C, C, dtype, false))) return st;
+  if (gate) {
+    if (N % rows_per_batch) return fail(HB_ERR_SHAPE, "gated_residual: N must be a multiple of rows_per_batch");
+    const bool several = N / rows_per_batch > 1;
+    if ((st = check_tensor("gated_residual", "gate", gate, several ? gate_batch_stride : C, C, dtype, true))) return st;
+  }
+  if (memory < 0) return fail(HB_ERR_SHAPE, "gated_residual: memory must be >= 0");
+  if (dtype == HB_BF16)
+    launch_residual<uint16_t>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local,
+                              memory, rows_per_batch, out, out_row_stride, N, C);
+  else if (dtype == HB_F16)
+    launch_residual<_Float16>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local,
+                              memory, rows_per_batch, out, out_row_stride, N, C);
+  else
+    launch_residual<float>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local, memory,
+                           rows_per_batch, out, out_row_stride, N, C);
+  return launched("gated_residual");
+}
+
+}  // extern "C"

@@ -20,6 +20,7 @@ import torch.nn.functional as F
 
 from hummingbird_amd import cross_attention as xattn
 from hummingbird_amd import dense_attention, projection, xla_chain
+from hummingbird_amd import elementwise as ew
 from hummingbird_amd.config import DiTConfig
 from hummingbird_amd.dtypes import Dtype
 
@@ -189,6 +190,9 @@ def block_forward(h: torch.Tensor, block: dict, static: dict, gcond: torch.Tenso
     compute = h.dtype
     scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff = (
         (block["to_scale_shift_gate"].to(compute) + gcond)[:, None, :]).chunk(6, dim=-1)
+    if use_hip(cfg, h):
+        return _block_fused(h, block, static, (scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff), index,
+                            cfg, projections)
     x = xla_chain.rms(h, block["pre_norm"]["weight"], cfg.norm_eps)
     x = x * (1 + scale_self) + shift_self
     x = self_attention(x, block, static, cfg, projections=projections)
@@ -205,6 +209,27 @@ def block_forward(h: torch.Tensor, block: dict, static: dict, gcond: torch.Tenso
     x = x * (1 + scale_ff) + shift_ff
     x = feed_forward(x, block["ff"])
     return h + x * torch.sigmoid(1 - gate_ff)
+
+
+def _block_fused(h: torch.Tensor, block: dict, static: dict, adaln: tuple, index: int, cfg: DiTConfig,
+                 projections: str) -> torch.Tensor:
+    """`block_forward` with the elementwise steps in HIP kernels, same cast points: `hb_rms_modulate` for the three
+    norms (with the adaLN modulation where the block has it), `hb_gated_residual` for the three residuals (the gates,
+    proj_out's bias and the local constant folded in), `hb_glu` for the SwiGLU with glu_proj's bias."""
+    scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff = (t[:, 0] for t in adaln)
+    x = ew.rms_modulate(h, block["pre_norm"]["weight"], cfg.norm_eps, scale_self, shift_self)
+    x = self_attention(x, block, static, cfg, projections=projections)
+    h = ew.gated_residual(h, x, gate=gate_self)
+
+    x = ew.rms_modulate(h, block["cross_attend_norm"]["weight"], cfg.norm_eps)
+    x = cross_attention(x, block, static["cross"][index], cfg)
+    h = ew.gated_residual(h, x, local=static["local"][index], memory=cfg.num_memory_tokens)
+
+    x = ew.rms_modulate(h, block["ff_norm"]["weight"], cfg.norm_eps, scale_ff, shift_ff)
+    ff = block["ff"]
+    x = ew.glu(linear(x, ff["glu_proj"]["weight"]), False, bias=ff["glu_proj"]["bias"])
+    x = linear(x, ff["proj_out"]["weight"])
+    return ew.gated_residual(h, x, gate=gate_ff, x_bias=ff["proj_out"]["bias"].to(h.dtype))
 
 
 def prepare_static(params: dict, cond: dict, padding_mask: torch.Tensor, cfg: DiTConfig, dtype: Dtype) -> dict:

@@ -1,7 +1,9 @@
-"""The elementwise steps of a SAME-L decoder block on MI355X (`hb_dyt`, `hb_glu`): the `attention="hip"`
-counterparts of `same_l._dyt` followed by the block's cast to the compute dtype (sa3jax/same_l.py:58-69,
-191-192) and of the GLU gate of `same_l._feed_forward` (sa3jax/same_l.py:172-183). Tensors are torch tensors on a
-ROCm device; work is enqueued on torch's current stream.
+"""The elementwise steps of a SAME-L decoder block (`hb_dyt`, `hb_glu`) and of a DiT block (`hb_rms_modulate`,
+`hb_gated_residual`) on MI355X: the `attention="hip"` counterparts of `same_l._dyt` followed by the block's cast to
+the compute dtype (sa3jax/same_l.py:58-69, 191-192), of the GLU gate of `same_l._feed_forward`
+(sa3jax/same_l.py:172-183; the DiT's SwiGLU, sa3jax/dit.py:218-221, is the same gate), and of the DiT block's
+norms, adaLN modulations and residuals (sa3jax/dit.py:224-251). Tensors are torch tensors on a ROCm device; work
+is enqueued on torch's current stream.
 """
 from __future__ import annotations
 
@@ -65,4 +67,72 @@ def glu(proj: torch.Tensor, sinusoidal: bool, bias: torch.Tensor | None = None) 
     stream = torch.cuda.current_stream(proj.device).cuda_stream
     _lib.check(_lib.load().hb_glu(stream, proj.data_ptr(), dtype_code(proj.dtype), stride, bias_p,
                                   int(bool(sinusoidal)), out.data_ptr(), inner, rows, inner), "glu")
+    return out
+
+
+def _per_batch(t: torch.Tensor | None, batch: int, channels: int, dtype: torch.dtype, name: str):
+    """(pointer, batch stride) of a `(B, C)` (or `(B, 1, C)`) per-batch row tensor in `dtype`, possibly a view into a
+    wider row (the adaLN chunks of `(B, 6 E)`); (0, 0) for None."""
+    if t is None:
+        return 0, 0
+    if t.dtype != dtype:
+        raise TypeError(f"{name} is {t.dtype}, expected {dtype}")
+    t2 = t.reshape(t.shape[0], t.shape[-1]) if t.dim() == 3 and t.shape[1] == 1 else t
+    if t2.dim() != 2 or tuple(t2.shape) != (batch, channels) or t2.stride(-1) != 1:
+        raise ValueError(f"{name} must be (B, C) = ({batch}, {channels}) with unit stride on C, got {tuple(t.shape)}")
+    return t2.data_ptr(), (t2.stride(0) if batch > 1 else channels)
+
+
+def rms_modulate(x: torch.Tensor, weight: torch.Tensor, eps: float, scale: torch.Tensor | None = None,
+                 shift: torch.Tensor | None = None) -> torch.Tensor:
+    """The DiT block norm on `(B, L, C)`: `cast(x * rsqrt(mean(x^2) + eps) * weight)` with an fp32 island
+    (sa3jax/dit.py:44-57), then with `scale` / `shift` `(B, C)` the adaLN modulation `* (1 + scale) + shift`
+    (sa3jax/dit.py:231-233, 246-247), each step in `x.dtype`. One pass (`hb_rms_modulate`)."""
+    _require_gpu(x, "x")
+    if x.dim() != 3:
+        raise ValueError(f"x must be (B, L, C), got {tuple(x.shape)}")
+    batch, length, channels = x.shape
+    rows, stride = _rows(x, "x")
+    w = weight.to(device=x.device, dtype=torch.float32).contiguous().reshape(-1)
+    if w.numel() != channels:
+        raise ValueError(f"weight must have {channels} elements")
+    if (scale is None) != (shift is None):
+        raise ValueError("scale and shift are given together or not at all")
+    sp, ms = _per_batch(scale, batch, channels, x.dtype, "scale")
+    hp, ms2 = _per_batch(shift, batch, channels, x.dtype, "shift")
+    if scale is not None and ms != ms2:
+        raise ValueError("scale and shift must share their batch stride")
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    _lib.check(_lib.load().hb_rms_modulate(stream, x.data_ptr(), dtype_code(x.dtype), stride, w.data_ptr(), float(eps),
+                                           sp, hp, ms, length, out.data_ptr(), channels, rows, channels),
+               "rms_modulate")
+    return out
+
+
+def gated_residual(h: torch.Tensor, x: torch.Tensor, gate: torch.Tensor | None = None,
+                   x_bias: torch.Tensor | None = None, local: torch.Tensor | None = None,
+                   memory: int = 0) -> torch.Tensor:
+    """`h + (x + x_bias) * sigmoid(1 - gate)` on `(B, L, C)` (sa3jax/dit.py:234, 249-251), or `h + x` without
+    `gate`, then `+ local` on the tokens at or past `memory` (sa3jax/dit.py:237-241); each step in `h.dtype`.
+    `gate` is `(B, C)`, `x_bias` and `local` `(C,)`. One pass (`hb_gated_residual`)."""
+    _require_gpu(h, "h")
+    if h.dim() != 3 or x.shape != h.shape or x.dtype != h.dtype:
+        raise ValueError(f"h and x must be (B, L, C) of one shape and dtype, got {tuple(h.shape)}, {tuple(x.shape)}")
+    batch, length, channels = h.shape
+    _, hs = _rows(h, "h")
+    rows, xs = _rows(x, "x")
+    gp, gs = _per_batch(gate, batch, channels, h.dtype, "gate")
+
+    def vec(t, name):
+        if t is None:
+            return 0
+        if t.dtype != h.dtype or t.numel() != channels or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be ({channels},) of {h.dtype} with unit stride")
+        return t.data_ptr()
+    out = torch.empty(h.shape, dtype=h.dtype, device=h.device)
+    stream = torch.cuda.current_stream(h.device).cuda_stream
+    _lib.check(_lib.load().hb_gated_residual(stream, h.data_ptr(), dtype_code(h.dtype), hs, x.data_ptr(), xs,
+                                             vec(x_bias, "x_bias"), gp, gs, vec(local, "local"), int(memory), length,
+                                             out.data_ptr(), channels, rows, channels), "gated_residual")
     return out

@@ -14,6 +14,8 @@
  *   hb_dit_qkv_proj,   replace   the GEMMs either side of the DiT kernel (sa3jax/dit.py:190, 195), the first with the
  *   hb_dense_attend_qq,          dense kernel's key preparation in its epilogue;
  *   hb_proj
+ *   hb_rms_modulate,   replace   the elementwise steps of dit._block around its GEMMs and attention calls
+ *   hb_gated_residual            (sa3jax/dit.py:224-251), an XLA chain in the reference;
  *   hb_rope_tables     replaces  band_attention.rope_tables / dit._rope_tables
  *                      (sa3jax/band_attention.py:43-58, sa3jax/dit.py:82-87) in a kernel-native layout.
  *
@@ -217,6 +219,30 @@ int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, c
            int64_t out_row_stride, int64_t N, int C);
 int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_stride, const float* bias,
            int sinusoidal, void* out, int64_t out_row_stride, int64_t N, int F);
+
+/* ---- DiT block: the elementwise steps around the GEMMs and attention calls ---------------------------------
+ * Replace the array operations of dit._block between its matmuls (sa3jax/dit.py:224-251).
+ *   hb_rms_modulate   : y = cast(x * rsqrt(mean(x^2) + eps) * weight), the block RMSNorm (sa3jax/dit.py:44-57:
+ *                       fp32 mean of squares, `weight` applied in fp32, cast back); with `scale` and `shift` (both
+ *                       or neither) then out = y * (1 + scale) + shift, the adaLN modulation (dit.py:231-233,
+ *                       246-247), each step rounded to the compute dtype; without them out = y (dit.py:236).
+ *                       scale, shift: one row of C values per batch, `mod_batch_stride` elements apart; row n of x
+ *                       belongs to batch n / rows_per_batch. weight: C floats.
+ *   hb_gated_residual : out = h + (x + x_bias) * sigmoid(1 - gate) (dit.py:234, 249-251; x_bias is proj_out's bias,
+ *                       dit.py:221), each step rounded to the compute dtype; without `gate` out = h + (x + x_bias);
+ *                       without `x_bias` the bias step is skipped; with `local` the constant local embedding is
+ *                       then added to the rows whose token index n % rows_per_batch is >= `memory` (dit.py:237-241).
+ *                       gate: one row of C values per batch, `gate_batch_stride` elements apart; x_bias, local: C
+ *                       values.
+ *   All tensors are of `dtype` (HB_BF16, HB_F16 or HB_F32) except `weight`; row strides in elements, multiples of
+ *   8 (bf16, half) or 4 (fp32); every pointer 16-byte aligned; C a multiple of 8 (bf16, half) or 4 (fp32). */
+int hb_rms_modulate(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const float* weight,
+                    float eps, const void* scale, const void* shift, int64_t mod_batch_stride, int rows_per_batch,
+                    void* out, int64_t out_row_stride, int64_t N, int C);
+int hb_gated_residual(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* x,
+                      int64_t x_row_stride, const void* x_bias, const void* gate, int64_t gate_batch_stride,
+                      const void* local, int memory, int rows_per_batch, void* out, int64_t out_row_stride,
+                      int64_t N, int C);
 
 #ifdef __cplusplus
 }

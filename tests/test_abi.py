@@ -178,3 +178,23 @@ def test_projection_entry_points_reject_before_any_launch(lib):
                                                  fake, fake, fake, 32, None, fake, B, L, H, D, 1e-6,
                                                  kw.get("ws", fake), kw.get("wsb", need))
     assert attend(rs=2 * H * D - 8) == 7 and attend(dtype=1) == 3 and attend(wsb=need - 1) == 8
+
+
+def test_dit_block_entry_points_reject_before_any_launch(lib):
+    """hb_rms_modulate and hb_gated_residual validate dtype, shapes, strides, alignment and their optional
+    operands on the host (fake, never dereferenced addresses)."""
+    fake = 0x100000
+    rms = lambda **kw: lib.hb_rms_modulate(  # noqa: E731
+        None, kw.get("x", fake), kw.get("dtype", 0), kw.get("xs", 64), kw.get("w", fake), kw.get("eps", 1e-5),
+        kw.get("scale", None), kw.get("shift", None), kw.get("ms", 384), kw.get("L", 10), fake, 64, kw.get("N", 20),
+        kw.get("C", 64))
+    assert rms(dtype=5) == 3 and rms(C=60) == 2 and rms(N=0) == 2 and rms(L=0) == 2
+    assert rms(xs=56) == 7 and rms(x=fake + 8) == 7 and rms(w=None) == 1 and rms(eps=-1.0) == 10
+    assert rms(scale=fake) == 1                      # scale without shift
+    assert rms(scale=fake, shift=fake, N=25) == 2    # rows not a whole number of batches
+    assert rms(scale=fake, shift=fake, ms=40) == 7   # batch stride below C
+    res = lambda **kw: lib.hb_gated_residual(  # noqa: E731
+        None, fake, kw.get("dtype", 0), 64, kw.get("x", fake), kw.get("xs", 64), kw.get("xb", None),
+        kw.get("gate", None), kw.get("gs", 64), kw.get("local", None), kw.get("memory", 0), 10, fake, 64, 20, 64)
+    assert res(dtype=9) == 3 and res(x=None) == 1 and res(xs=8) == 7 and res(xb=fake + 4) == 7
+    assert res(gate=fake, gs=32) == 7 and res(local=fake + 2) == 7 and res(memory=-1) == 2
