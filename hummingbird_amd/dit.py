@@ -183,13 +183,15 @@ def local_constants(blocks: list, compute: torch.dtype) -> torch.Tensor:
 
 
 def block_forward(h: torch.Tensor, block: dict, static: dict, gcond: torch.Tensor, index: int, cfg: DiTConfig,
-                  projections: str = "torch") -> torch.Tensor:
+                  projections: str = "torch", adaln: torch.Tensor | None = None) -> torch.Tensor:
     """One transformer block with adaLN (sa3jax/dit.py:224-251): `h + attn(rms(h) (1 + scale) + shift) *
     sigmoid(1 - gate)`, `h + cross(rms(h))`, the local constant on the latent tokens, then the feed-forward the
-    same way as the self-attention. `gcond` is `(B, 6 E)`."""
+    same way as the self-attention. `gcond` is `(B, 6 E)`; `adaln`, if given, is the block's
+    `to_scale_shift_gate + gcond` computed by the caller (the same values)."""
     compute = h.dtype
-    scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff = (
-        (block["to_scale_shift_gate"].to(compute) + gcond)[:, None, :]).chunk(6, dim=-1)
+    if adaln is None:
+        adaln = block["to_scale_shift_gate"].to(compute) + gcond
+    scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff = adaln[:, None, :].chunk(6, dim=-1)
     if use_hip(cfg, h):
         return _block_fused(h, block, static, (scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff), index,
                             cfg, projections)
@@ -232,6 +234,18 @@ def _block_fused(h: torch.Tensor, block: dict, static: dict, adaln: tuple, index
     return ew.gated_residual(h, x, gate=gate_ff, x_bias=ff["proj_out"]["bias"].to(h.dtype))
 
 
+def _fp32_norms(block: dict) -> dict:
+    """A view of a block's parameters with its norm scales in fp32 (the other tensors shared)."""
+    out = dict(block)
+    for key in ("pre_norm", "cross_attend_norm", "ff_norm"):
+        out[key] = {"weight": block[key]["weight"].float().contiguous()}
+    for attn in ("self_attn", "cross_attn"):
+        out[attn] = dict(block[attn])
+        for norm in ("q_norm", "k_norm"):
+            out[attn][norm] = {"weight": block[attn][norm]["weight"].float().contiguous()}
+    return out
+
+
 def prepare_static(params: dict, cond: dict, padding_mask: torch.Tensor, cfg: DiTConfig, dtype: Dtype) -> dict:
     """Everything `dit_forward` reads that does not depend on `x` or `t` (sa3jax/dit.py:287-337), built once per
     clip: the tables of `static_tables`, the projected context and every block's prepared cross-attention
@@ -251,6 +265,9 @@ def prepare_static(params: dict, cond: dict, padding_mask: torch.Tensor, cfg: Di
     static["cross"] = [cross_context(b, ctx, cfg) for b in net["blocks"]]
     static["gcond_proj"] = sequential(params["to_global_embed"], cond["global_cond"].to(compute))
     static["local"] = local_constants(net["blocks"], compute)
+    static["adaln"] = torch.stack([b["to_scale_shift_gate"].to(compute) for b in net["blocks"]])  # (depth, 6 E)
+    if cfg.attention == "hip":  # the kernels take the norm scales in fp32: convert them once per clip
+        static["blocks"] = [_fp32_norms(b) for b in net["blocks"]]
     if cfg.attention == "hip" and cfg.differential:
         batch, length = padding_mask.shape[0], cfg.num_memory_tokens + padding_mask.shape[1]
         need = dense_attention.workspace_bytes(compute, batch, length, cfg.num_heads, cfg.head_dim)
@@ -274,8 +291,11 @@ def dit_forward(params: dict, x: torch.Tensor, t: torch.Tensor, static: dict, cf
     timestep = sequential(params["to_timestep_embed"], expo_fourier(t.to(compute), cfg.fourier_dim))
     gcond = sequential(net["global_cond_embedder"], static["gcond_proj"] + timestep)
 
-    for index, block in enumerate(net["blocks"]):
-        h = block_forward(h, block, static, gcond, index, cfg, projections)
+    adaln = static["adaln"][:, None, :] + gcond[None] if "adaln" in static else None  # every block's, one launch
+    blocks = static.get("blocks", net["blocks"])
+    for index, block in enumerate(blocks):
+        h = block_forward(h, block, static, gcond, index, cfg, projections,
+                          adaln=None if adaln is None else adaln[index])
 
     h = linear(h[:, cfg.num_memory_tokens:, :], net["project_out"]["weight"])
     v = h.transpose(1, 2)
