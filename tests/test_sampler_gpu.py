@@ -4,9 +4,9 @@ sa3jax/sampling.py:81-118).
 * the denoiser (a 2-block DiT with 2 heads of 64) in fp32 against the oracle, and three sampler steps likewise
   (tolerance: 2e-5 of the output's largest magnitude; the attention calls alone hold 1e-5 relative, the GEMMs,
   norms and residuals around them add fp32 rounding of the same order);
-* the `medium` geometry (width 1536, 24 heads, 2 blocks, 300 latents, batch 2) in bf16 against attention="xla"
-  on the same device, with hipBLASLt and with this package's projection GEMMs, at the bf16 contract applied to
-  the output divided by its largest magnitude;
+* the `medium` geometry (width 1536, 24 heads, 2 blocks, 300 latents, batch 2) under the BF16 and FP16 presets
+  against attention="xla" on the same device, with hipBLASLt and with this package's projection GEMMs, at the bf16
+  contract applied to the output divided by its largest magnitude;
 * the whole sampler loop captured as a HIP graph against the eager loop: bit-identical on three replays with new
   inputs, with eager work and synchronisations in between.
 The timestep features are shared between the mirror and the oracle (oracle.dit.expo_fourier explains why).
@@ -21,7 +21,7 @@ import torch
 
 from hummingbird_amd import dit, sampling
 from hummingbird_amd.config import MEDIUM_DIT
-from hummingbird_amd.dtypes import BF16, FP32_PARITY
+from hummingbird_amd.dtypes import BF16, FP16, FP32_PARITY
 from oracle import dit as odit
 from tests.test_sampler import TINY, cond_case, to_np
 from tests.util import assert_bf16_parity, stats
@@ -89,18 +89,20 @@ def test_sampler_hip_fp32_vs_oracle():
 MEDIUM2 = dataclasses.replace(MEDIUM_DIT, depth=2)
 
 
-@pytest.mark.parametrize("projections", ["torch", "hip"])
-def test_dit_forward_medium_bf16_hip_vs_xla(projections):
-    announce(f"dit_forward medium bf16 hip ({projections} projections) vs xla")
-    params, cond, mask, x = case(MEDIUM2, BF16, 2, 300, seed=24, ctx_tokens=257)
+@pytest.mark.parametrize("projections,preset", [("torch", "bf16"), ("hip", "bf16"), ("torch", "fp16"),
+                                                ("hip", "fp16")])
+def test_dit_forward_medium_hip_vs_xla(projections, preset):
+    announce(f"dit_forward medium {preset} hip ({projections} projections) vs xla")
+    dtype = {"bf16": BF16, "fp16": FP16}[preset]
+    params, cond, mask, x = case(MEDIUM2, dtype, 2, 300, seed=24, ctx_tokens=257)
     t = torch.tensor([0.9, 0.35], device=DEV)
-    static = dit.prepare_static(params, cond, mask, MEDIUM2, BF16)
-    got = dit.dit_forward(params, x, t, static, MEDIUM2, BF16, projections=projections).float().cpu().numpy()
+    static = dit.prepare_static(params, cond, mask, MEDIUM2, dtype)
+    got = dit.dit_forward(params, x, t, static, MEDIUM2, dtype, projections=projections).float().cpu().numpy()
     xcfg = dataclasses.replace(MEDIUM2, attention="xla")
-    xstatic = dit.prepare_static(params, cond, mask, xcfg, BF16)
-    ref = dit.dit_forward(params, x, t, xstatic, xcfg, BF16).float().cpu().numpy()
+    xstatic = dit.prepare_static(params, cond, mask, xcfg, dtype)
+    ref = dit.dit_forward(params, x, t, xstatic, xcfg, dtype).float().cpu().numpy()
     scale = float(np.abs(ref).max())
-    assert_bf16_parity(got / scale, ref / scale, f"medium dit_forward ({projections}) / max")
+    assert_bf16_parity(got / scale, ref / scale, f"medium dit_forward {preset} ({projections}) / max")
 
 
 @pytest.mark.parametrize("projections", ["torch", "hip"])
