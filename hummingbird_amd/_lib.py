@@ -62,6 +62,9 @@ SIGNATURES = {
                                 c_int, c_void_p, c_int64, c_int64, c_int]),
     "hb_gated_residual": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
                                   c_void_p, c_int, c_int, c_void_p, c_int64, c_int64, c_int]),
+    "hb_residual_rms": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
+                                c_void_p, c_int, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_int, c_void_p,
+                                c_void_p, c_int64, c_int64, c_int]),
 }
 
 _lib: ctypes.CDLL | None = None

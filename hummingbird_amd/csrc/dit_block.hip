@@ -9,7 +9,10 @@
 //   gated_residual  out = h + (x + bias) * sigmoid(1 - gate): the gated residuals of the self-attention and the
 //                   feed-forward (dit.py:234, 249-251; the bias is proj_out's, dit.py:221), or the plain residual
 //                   of the cross-attention (dit.py:237) followed by the constant local embedding on the latent
-//                   tokens (dit.py:239-241).
+//                   tokens (dit.py:239-241);
+//   residual_rms    the two back to back on one row: a residual, then the norm (and modulation) that consumes it
+//                   (the cross-attention input after the self-attention residual, the feed-forward input after the
+//                   cross-attention residual, the next block's input after the feed-forward residual).
 // Each is one HBM pass over 16-byte chunks. bf16 and half round where the reference holds an array of the compute
 // dtype: after the norm, 1 + scale, the product, the shift; x + bias, 1 - gate, the sigmoid, the product, the
 // residual sum, the local sum. fp32 does not round.
@@ -148,6 +151,79 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(const T* __restrict
   }
 }
 
+// residual then norm of the same row, one wave per row with the row in registers (at most KMAX chunks per lane):
+// h' = the gated_residual of (h, x) with the same optional operands and roundings, stored; then
+// y = rms_modulate(h') with the same optional modulation, stored. The sum of squares runs over the rounded h' in
+// the order rms_modulate_kernel uses, so y equals what the two kernels produce one after the other.
+template <typename T, int KMAX>
+__global__ __launch_bounds__(256) void residual_rms_kernel(
+    const T* __restrict__ h, int64_t hs, const T* __restrict__ x, int64_t xs, const T* __restrict__ xbias,
+    const T* __restrict__ gate, int64_t gate_stride, const T* __restrict__ local, int memory,
+    const float* __restrict__ w, float eps, const T* __restrict__ scale, const T* __restrict__ shift,
+    int64_t mod_stride, int L, T* __restrict__ out_h, T* __restrict__ out_y, int64_t os, int64_t N, int C) {
+  constexpr int V = Vec<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + wave_id();
+  if (n >= N) return;  // wave-uniform
+  const int64_t b = n / L;
+  const bool latent = static_cast<int>(n - b * L) >= memory;
+  float r[KMAX][V];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int c0 = (lane + 64 * k) * V;
+    if (c0 >= C) break;
+    float xv[V];
+    Vec<T>::load(h + n * hs + c0, r[k]);
+    Vec<T>::load(x + n * xs + c0, xv);
+    if (xbias) {
+      float bv[V];
+      Vec<T>::load(xbias + c0, bv);
+#pragma unroll
+      for (int j = 0; j < V; ++j) xv[j] = Vec<T>::round(xv[j] + bv[j]);
+    }
+    if (gate) {
+      float g[V];
+      Vec<T>::load(gate + b * gate_stride + c0, g);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float u = Vec<T>::round(1.f - g[j]);
+        xv[j] = Vec<T>::round(xv[j] * Vec<T>::round(1.f / (1.f + expf(-u))));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) r[k][j] = Vec<T>::round(r[k][j] + xv[j]);
+    if (local && latent) {
+      float lv[V];
+      Vec<T>::load(local + c0, lv);
+#pragma unroll
+      for (int j = 0; j < V; ++j) r[k][j] = Vec<T>::round(r[k][j] + lv[j]);
+    }
+    Vec<T>::store(out_h + n * os + c0, r[k]);
+#pragma unroll
+    for (int j = 0; j < V; ++j) ss = ss + r[k][j] * r[k][j];
+  }
+  const float inv = rsqrtf(wave_sum(ss) * (1.f / static_cast<float>(C)) + eps);
+  const T* sc = scale ? scale + b * mod_stride : nullptr;
+  const T* sh = shift ? shift + b * mod_stride : nullptr;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int c0 = (lane + 64 * k) * V;
+    if (c0 >= C) break;
+    float v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = Vec<T>::round((r[k][j] * inv) * w[c0 + j]);
+    if (sc) {
+      float s[V], t[V];
+      Vec<T>::load(sc + c0, s);
+      Vec<T>::load(sh + c0, t);
+#pragma unroll
+      for (int j = 0; j < V; ++j) v[j] = Vec<T>::round(Vec<T>::round(v[j] * Vec<T>::round(1.f + s[j])) + t[j]);
+    }
+    Vec<T>::store(out_y + n * os + c0, v);
+  }
+}
+
 }  // namespace blk
 }  // namespace hb
 
@@ -203,6 +279,20 @@ void launch_residual(hipStream_t s, const void* h, int64_t hs, const void* x, in
                      0, s, static_cast<const T*>(h), hs, static_cast<const T*>(x), xs, static_cast<const T*>(xbias),
                      static_cast<const T*>(gate), gs, static_cast<const T*>(local), memory, L, static_cast<T*>(out), os,
                      N, C);
+}
+
+constexpr int kResidualRmsChunks = 4;  // chunks of 16 bytes per lane: C <= 2048 (bf16, half) or 1024 (fp32)
+
+template <typename T>
+void launch_residual_rms(hipStream_t s, const void* h, int64_t hs, const void* x, int64_t xs, const void* xbias,
+                         const void* gate, int64_t gs, const void* local, int memory, const float* w, float eps,
+                         const void* scale, const void* shift, int64_t ms, int L, void* out_h, void* out_y, int64_t os,
+                         int64_t N, int C) {
+  hipLaunchKernelGGL((blk::residual_rms_kernel<T, kResidualRmsChunks>), dim3(static_cast<unsigned>((N + 3) / 4)),
+                     dim3(256), 0, s, static_cast<const T*>(h), hs, static_cast<const T*>(x), xs,
+                     static_cast<const T*>(xbias), static_cast<const T*>(gate), gs, static_cast<const T*>(local), memory,
+                     w, eps, static_cast<const T*>(scale), static_cast<const T*>(shift), ms, L, static_cast<T*>(out_h),
+                     static_cast<T*>(out_y), os, N, C);
 }
 
 }  // namespace
@@ -266,6 +356,51 @@ int hb_gated_residual(hipStream_t stream, const void* h, int dtype, int64_t h_ro
     launch_residual<float>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local, memory,
                            rows_per_batch, out, out_row_stride, N, C);
   return launched("gated_residual");
+}
+
+int hb_residual_rms(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* x,
+                    int64_t x_row_stride, const void* x_bias, const void* gate, int64_t gate_batch_stride,
+                    const void* local, int memory, const float* weight, float eps, const void* scale,
+                    const void* shift, int64_t mod_batch_stride, int rows_per_batch, void* out_h, void* out_y,
+                    int64_t out_row_stride, int64_t N, int C) {
+  clear_error();
+  int st = check_common("residual_rms", dtype, N, C, rows_per_batch);
+  if (st) return st;
+  if (C > 64 * vec_of(dtype) * kResidualRmsChunks)
+    return fail(HB_ERR_SHAPE, "residual_rms holds a row in registers: C (%d) must be <= %d", C,
+                64 * vec_of(dtype) * kResidualRmsChunks);
+  if ((st = check_tensor("residual_rms", "h", h, h_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("residual_rms", "x", x, x_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("residual_rms", "out_h", out_h, out_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("residual_rms", "out_y", out_y, out_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("residual_rms", "x_bias", x_bias, C, C, dtype, false))) return st;
+  if ((st = check_tensor("residual_rms", "local", local, C, C, dtype, false))) return st;
+  if (!weight) return fail(HB_ERR_NULL, "residual_rms: weight must be non-NULL");
+  if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(HB_ERR_EPS, "residual_rms: eps %g must be finite and >= 0", eps);
+  if (!scale != !shift) return fail(HB_ERR_NULL, "residual_rms: scale and shift are given together or not at all");
+  if (memory < 0) return fail(HB_ERR_SHAPE, "residual_rms: memory must be >= 0");
+  if (gate || scale) {
+    if (N % rows_per_batch) return fail(HB_ERR_SHAPE, "residual_rms: N must be a multiple of rows_per_batch");
+    const bool several = N / rows_per_batch > 1;
+    if (gate && (st = check_tensor("residual_rms", "gate", gate, several ? gate_batch_stride : C, C, dtype, true)))
+      return st;
+    if (scale && ((st = check_tensor("residual_rms", "scale", scale, several ? mod_batch_stride : C, C, dtype, true)) ||
+                  (st = check_tensor("residual_rms", "shift", shift, several ? mod_batch_stride : C, C, dtype, true))))
+      return st;
+  }
+  if (dtype == HB_BF16)
+    launch_residual_rms<uint16_t>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local,
+                                  memory, weight, eps, scale, shift, mod_batch_stride, rows_per_batch, out_h, out_y,
+                                  out_row_stride, N, C);
+  else if (dtype == HB_F16)
+    launch_residual_rms<_Float16>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local,
+                                  memory, weight, eps, scale, shift, mod_batch_stride, rows_per_batch, out_h, out_y,
+                                  out_row_stride, N, C);
+  else
+    launch_residual_rms<float>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local,
+                               memory, weight, eps, scale, shift, mod_batch_stride, rows_per_batch, out_h, out_y,
+                               out_row_stride, N, C);
+  return launched("residual_rms");
 }
 
 }  // extern "C"

@@ -213,6 +213,38 @@ def block_forward(h: torch.Tensor, block: dict, static: dict, gcond: torch.Tenso
     return h + x * torch.sigmoid(1 - gate_ff)
 
 
+def _blocks_fused(h: torch.Tensor, blocks: list, static: dict, adaln: torch.Tensor, cfg: DiTConfig,
+                  projections: str) -> torch.Tensor:
+    """Every block of `dit_forward` with the elementwise steps in HIP kernels, residual and following norm fused
+    (`hb_residual_rms`): the feed-forward residual of block i computes block i + 1's modulated input in the same
+    pass. Same values as `block_forward` block after block. `adaln` is `(depth, B, 6 E)`."""
+    eps, E = cfg.norm_eps, h.shape[-1]
+    depth = len(blocks)
+
+    def chunks(i):
+        return adaln[i].reshape(adaln.shape[1], 6, E).unbind(1)  # (B, E) views: scale, shift, gate x 2
+    s_self, sh_self, g_self, s_ff, sh_ff, g_ff = chunks(0)
+    x = ew.rms_modulate(h, blocks[0]["pre_norm"]["weight"], eps, s_self, sh_self)
+    for i, block in enumerate(blocks):
+        s_self, sh_self, g_self, s_ff, sh_ff, g_ff = chunks(i)
+        a = self_attention(x, block, static, cfg, projections=projections)
+        h, x = ew.residual_rms(h, a, block["cross_attend_norm"]["weight"], eps, gate=g_self)
+        c = cross_attention(x, block, static["cross"][i], cfg)
+        h, x = ew.residual_rms(h, c, block["ff_norm"]["weight"], eps, local=static["local"][i],
+                               memory=cfg.num_memory_tokens, scale=s_ff, shift=sh_ff)
+        ff = block["ff"]
+        f = linear(ew.glu(linear(x, ff["glu_proj"]["weight"]), False, bias=ff["glu_proj"]["bias"]),
+                   ff["proj_out"]["weight"])
+        bias = ff["proj_out"]["bias"].to(h.dtype)
+        if i + 1 < depth:
+            ns, nsh = chunks(i + 1)[:2]
+            h, x = ew.residual_rms(h, f, blocks[i + 1]["pre_norm"]["weight"], eps, gate=g_ff, x_bias=bias, scale=ns,
+                                   shift=nsh)
+        else:
+            h = ew.gated_residual(h, f, gate=g_ff, x_bias=bias)
+    return h
+
+
 def _block_fused(h: torch.Tensor, block: dict, static: dict, adaln: tuple, index: int, cfg: DiTConfig,
                  projections: str) -> torch.Tensor:
     """`block_forward` with the elementwise steps in HIP kernels, same cast points: `hb_rms_modulate` for the three
@@ -293,9 +325,12 @@ def dit_forward(params: dict, x: torch.Tensor, t: torch.Tensor, static: dict, cf
 
     adaln = static["adaln"][:, None, :] + gcond[None] if "adaln" in static else None  # every block's, one launch
     blocks = static.get("blocks", net["blocks"])
-    for index, block in enumerate(blocks):
-        h = block_forward(h, block, static, gcond, index, cfg, projections,
-                          adaln=None if adaln is None else adaln[index])
+    if adaln is not None and blocks and use_hip(cfg, h) and ew.residual_rms_supported(h.dtype, cfg.embed_dim):
+        h = _blocks_fused(h, blocks, static, adaln, cfg, projections)
+    else:
+        for index, block in enumerate(blocks):
+            h = block_forward(h, block, static, gcond, index, cfg, projections,
+                              adaln=None if adaln is None else adaln[index])
 
     h = linear(h[:, cfg.num_memory_tokens:, :], net["project_out"]["weight"])
     v = h.transpose(1, 2)

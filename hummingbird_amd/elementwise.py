@@ -136,3 +136,50 @@ def gated_residual(h: torch.Tensor, x: torch.Tensor, gate: torch.Tensor | None =
                                              vec(x_bias, "x_bias"), gp, gs, vec(local, "local"), int(memory), length,
                                              out.data_ptr(), channels, rows, channels), "gated_residual")
     return out
+
+
+def residual_rms(h: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float,
+                 gate: torch.Tensor | None = None, x_bias: torch.Tensor | None = None,
+                 local: torch.Tensor | None = None, memory: int = 0, scale: torch.Tensor | None = None,
+                 shift: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """`gated_residual(h, x, gate, x_bias, local, memory)` and then `rms_modulate` of its result with `weight`, `eps`,
+    `scale`, `shift`, in one pass per row (`hb_residual_rms`; rows of at most 2048 bf16 / half or 1024 fp32 values):
+    returns `(h', norm(h'))`, the same values as the two calls. A DiT block's residuals each feed the next norm
+    (sa3jax/dit.py:234-236, 237-247, 249-251 into the next block's 231-233)."""
+    _require_gpu(h, "h")
+    if h.dim() != 3 or x.shape != h.shape or x.dtype != h.dtype:
+        raise ValueError(f"h and x must be (B, L, C) of one shape and dtype, got {tuple(h.shape)}, {tuple(x.shape)}")
+    batch, length, channels = h.shape
+    _, hs = _rows(h, "h")
+    rows, xs = _rows(x, "x")
+    gp, gs = _per_batch(gate, batch, channels, h.dtype, "gate")
+    if (scale is None) != (shift is None):
+        raise ValueError("scale and shift are given together or not at all")
+    sp, ms = _per_batch(scale, batch, channels, h.dtype, "scale")
+    hp, ms2 = _per_batch(shift, batch, channels, h.dtype, "shift")
+    if scale is not None and ms != ms2:
+        raise ValueError("scale and shift must share their batch stride")
+    w = weight.to(device=h.device, dtype=torch.float32).contiguous().reshape(-1)
+    if w.numel() != channels:
+        raise ValueError(f"weight must have {channels} elements")
+
+    def vec(t, name):
+        if t is None:
+            return 0
+        if t.dtype != h.dtype or t.numel() != channels or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be ({channels},) of {h.dtype} with unit stride")
+        return t.data_ptr()
+    out_h = torch.empty(h.shape, dtype=h.dtype, device=h.device)
+    out_y = torch.empty(h.shape, dtype=h.dtype, device=h.device)
+    stream = torch.cuda.current_stream(h.device).cuda_stream
+    _lib.check(_lib.load().hb_residual_rms(stream, h.data_ptr(), dtype_code(h.dtype), hs, x.data_ptr(), xs,
+                                           vec(x_bias, "x_bias"), gp, gs, vec(local, "local"), int(memory),
+                                           w.data_ptr(), float(eps), sp, hp, ms, length, out_h.data_ptr(),
+                                           out_y.data_ptr(), channels, rows, channels), "residual_rms")
+    return out_h, out_y
+
+
+def residual_rms_supported(dtype: torch.dtype, channels: int) -> bool:
+    """Whether `residual_rms` takes rows of `channels` values of `dtype` (held in registers)."""
+    per_row = 2048 if dtype in (torch.bfloat16, torch.float16) else 1024
+    return channels <= per_row and channels % (8 if per_row == 2048 else 4) == 0

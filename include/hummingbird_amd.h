@@ -15,7 +15,8 @@
  *   hb_dense_attend_qq,          dense kernel's key preparation in its epilogue;
  *   hb_proj
  *   hb_rms_modulate,   replace   the elementwise steps of dit._block around its GEMMs and attention calls
- *   hb_gated_residual            (sa3jax/dit.py:224-251), an XLA chain in the reference;
+ *   hb_gated_residual,           (sa3jax/dit.py:224-251), an XLA chain in the reference;
+ *   hb_residual_rms
  *   hb_rope_tables     replaces  band_attention.rope_tables / dit._rope_tables
  *                      (sa3jax/band_attention.py:43-58, sa3jax/dit.py:82-87) in a kernel-native layout.
  *
@@ -243,6 +244,15 @@ int hb_gated_residual(hipStream_t stream, const void* h, int dtype, int64_t h_ro
                       int64_t x_row_stride, const void* x_bias, const void* gate, int64_t gate_batch_stride,
                       const void* local, int memory, int rows_per_batch, void* out, int64_t out_row_stride,
                       int64_t N, int C);
+/*   hb_residual_rms   : hb_gated_residual into out_h, then hb_rms_modulate of out_h into out_y, in one pass that
+ *                       holds the row in registers (C <= 2048 for bf16 and half, 1024 for fp32); out_h and out_y
+ *                       share out_row_stride. The block's three residuals each feed a norm (dit.py:234-236,
+ *                       237-247, and 249-251 into the next block's 231-233). */
+int hb_residual_rms(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* x,
+                    int64_t x_row_stride, const void* x_bias, const void* gate, int64_t gate_batch_stride,
+                    const void* local, int memory, const float* weight, float eps, const void* scale,
+                    const void* shift, int64_t mod_batch_stride, int rows_per_batch, void* out_h, void* out_y,
+                    int64_t out_row_stride, int64_t N, int C);
 
 #ifdef __cplusplus
 }

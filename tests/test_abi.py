@@ -198,3 +198,16 @@ def test_dit_block_entry_points_reject_before_any_launch(lib):
         kw.get("gate", None), kw.get("gs", 64), kw.get("local", None), kw.get("memory", 0), 10, fake, 64, 20, 64)
     assert res(dtype=9) == 3 and res(x=None) == 1 and res(xs=8) == 7 and res(xb=fake + 4) == 7
     assert res(gate=fake, gs=32) == 7 and res(local=fake + 2) == 7 and res(memory=-1) == 2
+
+
+def test_residual_rms_rejects_before_any_launch(lib):
+    fake = 0x100000
+    call = lambda **kw: lib.hb_residual_rms(  # noqa: E731
+        None, fake, kw.get("dtype", 0), kw.get("C", 64), fake, kw.get("C", 64), None, kw.get("gate", None), 384,
+        None, 0, kw.get("w", fake), 1e-5, kw.get("scale", None), kw.get("shift", None), 384, 10,
+        kw.get("oh", fake), fake, kw.get("C", 64), kw.get("N", 20), kw.get("C", 64))
+    assert call(C=4096) == 2                  # the row must fit in registers
+    assert call(dtype=1, C=2048) == 2         # fp32 rows up to 1024
+    assert call(w=None) == 1 and call(scale=fake) == 1 and call(oh=None) == 1
+    assert call(gate=fake, N=25) == 2         # not a whole number of batches
+    assert call(dtype=4) == 3

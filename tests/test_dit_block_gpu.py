@@ -121,3 +121,31 @@ def test_gated_residual_vs_oracle(name, B, L, C, mode):
     if local is not None:
         mirror = torch.cat([mirror[:, :memory], mirror[:, memory:] + local], dim=1)
     check(got, mirror.float().cpu().numpy(), name, "gated_residual vs torch ops", operands)
+
+
+@pytest.mark.parametrize("name", list(DTYPES))
+@pytest.mark.parametrize("B,L,C,mode", [(2, 37, 64, "gate"), (1, 1422, 1536, "gate_bias_mod"),
+                                        (2, 300, 1536, "local_mod"), (3, 70, 1024, "plain")])
+def test_residual_rms_equals_the_two_kernels(name, B, L, C, mode):
+    """hb_residual_rms against hb_gated_residual followed by hb_rms_modulate on the same inputs: bit-identical (the
+    same roundings, the mean of squares in the same order); both of those are held to the oracle above."""
+    announce(f"residual_rms {name} B={B} L={L} C={C} {mode}")
+    dtype = DTYPES[name][0]
+    if name == "fp32" and C > 1024:
+        pytest.skip("fp32 rows of more than 1024 values are not held in registers")
+    gen = torch.Generator(device=DEV).manual_seed(3 * B * L + C)
+    h = rand((B, L, C), gen, dtype, std=3.0)
+    x = rand((B, L, C), gen, dtype)
+    ssg = rand((B, 6 * C), gen, dtype, std=0.5)
+    w = 1 + 0.1 * torch.randn(C, device=DEV, generator=gen)
+    gate = ssg[:, 2 * C:3 * C] if mode.startswith("gate") else None
+    xb = rand((C,), gen, dtype, std=0.1) if "bias" in mode else None
+    local = rand((C,), gen, dtype, std=0.5) if mode.startswith("local") else None
+    memory = 16 if local is not None else 0
+    scale, shift = (ssg[:, :C], ssg[:, C:2 * C]) if mode.endswith("mod") else (None, None)
+    got_h, got_y = ew.residual_rms(h, x, w, 1e-5, gate=gate, x_bias=xb, local=local, memory=memory, scale=scale,
+                                   shift=shift)
+    ref_h = ew.gated_residual(h, x, gate=gate, x_bias=xb, local=local, memory=memory)
+    ref_y = ew.rms_modulate(ref_h, w, 1e-5, scale, shift)
+    assert torch.equal(got_h, ref_h), "residual differs"
+    assert torch.equal(got_y, ref_y), f"norm differs: {(got_y != ref_y).sum().item()} elements"
