@@ -65,6 +65,10 @@ DenseLayout band_tiled_layout(int B, int S, int H, int D);
 int launch_band_tiled(hipStream_t stream, int dtype, const void* qkv, int64_t rs, const float* q_dyt, const float* k_dyt,
                       const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                       int S, int H, int D, void* workspace);
+// fp32 band with its keys prepared once into a workspace of dense_layout(HB_F32, B, S, H, D).total_bytes.
+int launch_band_f32_ws(hipStream_t stream, const void* qkv, int64_t rs, const float* qdyt, const float* kdyt,
+                       const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
+                       int S, int H, int D, void* workspace);
 int launch_band_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qdyt, const float* kdyt,
                     const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
                     int S, int H, int D);

@@ -6,7 +6,8 @@
 //     whole key window of a 64-query step in LDS and prepares every key once per run; no workspace;
 //   - bf16 or half, w > 128 or head_dim 128: the tiled kernels (band_tiled.hip), which prepare the keys into a
 //     caller-supplied workspace and stream each 128-query block's window through LDS;
-//   - fp32: the fp32 kernel (fp32.hip); no workspace.
+//   - fp32: the fp32 kernels (fp32.hip): with a workspace every key is prepared once and the attention streams the
+//     prepared tiles; without one (NULL, as before) each query block prepares its own window.
 #include "api.h"
 
 using namespace hb;
@@ -15,9 +16,11 @@ static bool band_needs_workspace(int dtype, int D, int half, int window) {
   return dtype != HB_F32 && !band_ring_supported(dtype, D, half, window);
 }
 
+// fp32: the workspace of the prepared keys, which the call uses when it is given one (it is optional there).
 extern "C" size_t hb_band_workspace_size(int dtype, int B, int S, int H, int D, int half, int window) {
   if ((dtype != HB_BF16 && dtype != HB_F32 && dtype != HB_F16) || B < 1 || S < 1 || H < 1 || (D != 64 && D != 128))
     return 0;
+  if (dtype == HB_F32) return dense_layout(HB_F32, B, S, H, D).total_bytes;
   if (!band_needs_workspace(dtype, D, half, window > S ? S : window)) return 0;
   return band_tiled_layout(B, S, H, D).total_bytes;
 }
@@ -38,6 +41,13 @@ extern "C" int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, 
     return fail(HB_ERR_STRIDE, "cos and sin must be 16-byte aligned");
   if (dtype == HB_F32) {
     if (reinterpret_cast<uintptr_t>(out) % 16) return fail(HB_ERR_STRIDE, "fp32 out must be 16-byte aligned");
+    if (workspace) {
+      const size_t need = dense_layout(HB_F32, B, S, H, D).total_bytes;
+      if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(HB_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+      if (workspace_bytes < need) return fail(HB_ERR_WORKSPACE, "workspace holds %zu bytes, needs %zu", workspace_bytes, need);
+      return launch_band_f32_ws(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D,
+                                workspace);
+    }
     return launch_band_f32(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D);
   }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");

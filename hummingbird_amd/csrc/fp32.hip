@@ -15,7 +15,9 @@
 // Work split: a workgroup (4 waves) owns 64 queries of one (batch, head); waves 0-1 run branch 1 on 32 queries
 // each, waves 2-3 branch 2, and the branch-2 waves hand lam * O2 / l2 to the branch-1 waves through LDS. Keys
 // stream through LDS in 64-key tiles (K, K_diff, V). The dense kernel reads the fp32 workspace written by its
-// prep kernel; the band kernel prepares its K / K_diff tiles itself (DyT with the device tanhf, RoPE).
+// prep kernel. The band call prepares every key once into a workspace (band_keys_f32: DyT with the device tanhf,
+// RoPE) and streams the prepared tiles (band_attend_ws_f32); without a workspace it prepares the K / K_diff tiles
+// of each query block's window itself (band_attend_f32).
 #include "api.h"
 #include "attn_tile.h"
 #include "common.h"
@@ -291,14 +293,14 @@ __global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict_
 }
 
 // DyT (same_l.py:58-69) and RoPE (same_l.py:92-100) in fp32 of two tensors (sections secA, secB) for the 64
-// positions pos0 .. pos0+63 into LDS rows (pitch KP); positions outside [0, S) give zero rows.
-// `dyt` = [alpha, gamma[0..D), beta[0..D)].
-template <int D>
+// positions pos0 .. pos0+63 into rows of pitch P floats (LDS rows by default, or workspace rows); positions
+// outside [0, S) give zero rows. `dyt` = [alpha, gamma[0..D), beta[0..D)].
+template <int D, int P = F32Tile<D>::KP>
 __device__ __forceinline__ void band_prep_f32(const float* __restrict__ xb, int64_t rs, int64_t offA, int64_t offB,
                                               int pos0, int S, int half, const float* __restrict__ dyt,
                                               const float* __restrict__ cosT, const float* __restrict__ sinT,
                                               float* __restrict__ dA, float* __restrict__ dB) {
-  constexpr int PAIRS = D / 16, TASKS = 64 * PAIRS / 256, KP = F32Tile<D>::KP;
+  constexpr int PAIRS = D / 16, TASKS = 64 * PAIRS / 256, KP = P;
   const int h8 = half / 8;
   const float alpha = dyt[0];
   const float* gamma = dyt + 1;
@@ -400,6 +402,86 @@ __global__ __launch_bounds__(256) void band_attend_f32(const float* __restrict__
   store_diff_f32<D>(smem, o, lsum, br, lam ? lam[h] : 1.f, orow);
 }
 
+// The keys of the band prepared once: DyT and RoPE of k and k_diff (the same steps as band_prep_f32 inside
+// band_attend_f32) and V as it is, for 64-key tile blockIdx.x of (batch blockIdx.z, head blockIdx.y), into the
+// fp32 workspace regions k', k_diff', v' (rows of D floats, Sp rows per (batch, head), zeros past S).
+template <int D>
+__global__ __launch_bounds__(256) void band_keys_f32(const float* __restrict__ qkv, int64_t rs, int S, int Sp, int H,
+                                                     const float* __restrict__ kdyt, const float* __restrict__ cosT,
+                                                     const float* __restrict__ sinT, int half, int64_t region,
+                                                     float* __restrict__ ws) {
+  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t HD = static_cast<int64_t>(H) * D, bh = static_cast<int64_t>(b) * H + h;
+  const float* xb = qkv + static_cast<int64_t>(b) * S * rs + h * D;
+  float* kA = ws + (bh * Sp + 64 * t) * D;
+  band_prep_f32<D, D>(xb, rs, HD, 4 * HD, 64 * t, S, half, kdyt, cosT, sinT, kA, kA + region);
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) {
+    const int ch = threadIdx.x + 256 * i, row = ch / (D / 4), col = (ch % (D / 4)) * 4, pos = 64 * t + row;
+    st4(ws + 2 * region + (bh * Sp + pos) * D + col,
+        pos < S ? ld4(xb + static_cast<int64_t>(pos) * rs + 2 * HD + col) : f32x4{0.f, 0.f, 0.f, 0.f});
+  }
+}
+
+// band_attend_f32 over prepared keys: the 64-aligned key tiles that meet the block's band are loaded from the
+// workspace of band_keys_f32 instead of being prepared per query block.
+template <int D>
+__global__ __launch_bounds__(256) void band_attend_ws_f32(const float* __restrict__ qkv, int64_t rs, int B, int S,
+                                                          int Sp, int H, int w, const float* __restrict__ qdyt,
+                                                          const float* __restrict__ cosT,
+                                                          const float* __restrict__ sinT, int half,
+                                                          const float* __restrict__ ws, int64_t region,
+                                                          const float* __restrict__ lam, float* __restrict__ out) {
+  using T = F32Tile<D>;
+  __shared__ __attribute__((aligned(16))) float smem[T::LDS_FLOATS];
+  // query-block-major order: the heads of one query block run together and share key rows in L2
+  const int qb = blockIdx.x / (B * H), bh = blockIdx.x % (B * H), h = bh % H, b = bh / H;
+  const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
+  const int br = wave >> 1, q0 = qb * 64, qw0 = q0 + (wave & 1) * 32, q = qw0 + lr;
+  const int64_t HD = static_cast<int64_t>(H) * D;
+  const float* xb = qkv + static_cast<int64_t>(b) * S * rs + h * D;
+
+  band_prep_f32<D>(xb, rs, 0, 3 * HD, q0, S, half, qdyt, cosT, sinT, smem, smem + T::TILE);
+  __syncthreads();
+  float qreg[D / 2];
+  const float* qrow = smem + br * T::TILE + ((wave & 1) * 32 + lr) * T::KP + lh * (D / 2);
+#pragma unroll
+  for (int j4 = 0; j4 < D / 8; ++j4) {
+    const f32x4 v = ld4(qrow + 4 * j4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qreg[4 * j4 + e] = v[e];
+  }
+  __syncthreads();
+
+  f32x16 o[D / 32];
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt) o[dt] = f32x16{};
+  float lsum = 0.f, m = -INFINITY;
+  const float c = kLog2e / sqrtf(static_cast<float>(D));
+  const int64_t rowbase = static_cast<int64_t>(bh) * Sp;
+  const float* src[3] = {ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D};
+  const int kbeg = (q0 - w > 0 ? q0 - w : 0) / 64 * 64;
+  const int kend = q0 + 64 + w < S ? q0 + 64 + w : S;
+  for (int k0 = kbeg; k0 < kend; k0 += 64) {  // k0 + 63 < Sp: Sp is a multiple of 128 and k0 < S
+#pragma unroll
+    for (int s3 = 0; s3 < 3; ++s3)
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        const int ch = threadIdx.x + 256 * i, row = ch / (D / 4), col = (ch % (D / 4)) * 4;
+        st4(smem + s3 * T::TILE + row * T::KP + col, ld4(src[s3] + static_cast<int64_t>(k0 + row) * D + col));
+      }
+    __syncthreads();
+    if (k0 <= qw0 + 31 + w && k0 + 63 >= qw0 - w)
+      attend_tile_f32<D>(smem + br * T::TILE, smem + 2 * T::TILE, qreg, o, lsum, m, c, [&](int k) {
+        const int kk = k0 + k, dist = kk - q;
+        return kk < S && dist <= w && -dist <= w;
+      });
+    __syncthreads();
+  }
+  float* orow = q < S ? out + (static_cast<int64_t>(b) * S + q) * HD + h * D : nullptr;
+  store_diff_f32<D>(smem, o, lsum, br, lam ? lam[h] : 1.f, orow);
+}
+
 static int launched(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(HB_ERR_LAUNCH, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -438,6 +520,30 @@ int launch_dense_attend_f32(hipStream_t stream, const void* qkv, int64_t rs, int
     hipLaunchKernelGGL(dense_attend_f32<128>, dim3(nblocks), dim3(256), 0, stream, x, rs, sqd, qw, cosT, sinT, half,
                        eps, w, lay.region_elems, B, L, Lp, Lk, Lkp, H, lam, o);
   return launched("dense_attend_f32");
+}
+
+int launch_band_f32_ws(hipStream_t stream, const void* qkv, int64_t rs, const float* qdyt, const float* kdyt,
+                       const float* cosT, const float* sinT, int half, int window, const float* lam, void* out, int B,
+                       int S, int H, int D, void* workspace) {
+  const DenseLayout lay = dense_layout(HB_F32, B, S, H, D);
+  const int Sp = static_cast<int>(lay.Lp);
+  const float* x = static_cast<const float*>(qkv);
+  float* ws = static_cast<float*>(workspace);
+  float* o = static_cast<float*>(out);
+  const dim3 kgrid(static_cast<unsigned>(Sp / 64), static_cast<unsigned>(H), static_cast<unsigned>(B));
+  const int nblocks = B * H * ((S + 63) / 64);
+  if (D == 64) {
+    hipLaunchKernelGGL(band_keys_f32<64>, kgrid, dim3(256), 0, stream, x, rs, S, Sp, H, kdyt, cosT, sinT, half,
+                       lay.region_elems, ws);
+    hipLaunchKernelGGL(band_attend_ws_f32<64>, dim3(nblocks), dim3(256), 0, stream, x, rs, B, S, Sp, H, window, qdyt,
+                       cosT, sinT, half, ws, lay.region_elems, lam, o);
+  } else {
+    hipLaunchKernelGGL(band_keys_f32<128>, kgrid, dim3(256), 0, stream, x, rs, S, Sp, H, kdyt, cosT, sinT, half,
+                       lay.region_elems, ws);
+    hipLaunchKernelGGL(band_attend_ws_f32<128>, dim3(nblocks), dim3(256), 0, stream, x, rs, B, S, Sp, H, window,
+                       qdyt, cosT, sinT, half, ws, lay.region_elems, lam, o);
+  }
+  return launched("band_attend_ws_f32");
 }
 
 int launch_band_f32(hipStream_t stream, const void* qkv, int64_t rs, const float* qdyt, const float* kdyt,

@@ -165,10 +165,13 @@ int hb_proj(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, 
  *   cos, sin     : (S, half) floats from hb_rope_tables (ignored when half == 0)
  *   dtype        : HB_BF16, HB_F16 or HB_F32;  D: 64 or 128;  0 <= half <= D/2 with half % 8 == 0;  window >= 0
  *   workspace    : >= hb_band_workspace_size(dtype, B, S, H, D, half, window) bytes, 256-byte aligned; that size
- *                  is 0 (and workspace may be NULL) for fp32 and for 16-bit inputs with D = 64 and window <= 128, which
- *                  run without one. Otherwise it holds the prepared keys for the duration of the call.
- * Kernels: 16-bit inputs with D = 64 and window <= 128 run one streaming kernel; other 16-bit shapes run a key
- * preparation kernel and an attention kernel over the workspace; fp32 runs one kernel. */
+ *                  is 0 (and workspace may be NULL) for 16-bit inputs with D = 64 and window <= 128, which run
+ *                  without one. For fp32 the workspace is optional: given, it holds the prepared keys; NULL runs the
+ *                  kernel that prepares each query block's key window itself. Otherwise it holds the prepared keys
+ *                  for the duration of the call.
+ * Kernels: 16-bit inputs with D = 64 and window <= 128 run one streaming kernel; other 16-bit shapes, and fp32 with
+ * a workspace, run a key preparation kernel and an attention kernel over the workspace; fp32 without one runs one
+ * kernel. */
 size_t hb_band_workspace_size(int dtype, int B, int S, int H, int D, int half, int window);
 int hb_band_validate(int dtype, int64_t row_stride, int B, int S, int H, int D, int half, int window);
 int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride,

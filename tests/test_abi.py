@@ -129,7 +129,9 @@ def test_workspace_and_alignment_errors_before_any_launch(lib):
     # bf16 with a window beyond the streaming kernel needs a workspace: missing or short ones are rejected
     need = lib.hb_band_workspace_size(0, B, L, H, D, 32, 200)
     assert need == 3 * B * H * 256 * D * 2
-    assert lib.hb_band_workspace_size(0, B, L, H, D, 32, 128) == 0 and lib.hb_band_workspace_size(1, B, L, H, D, 32, 200) == 0
+    assert lib.hb_band_workspace_size(0, B, L, H, D, 32, 128) == 0
+    # fp32: the optional workspace of the prepared keys, three fp32 (B, H, round_up(S, 128), D) regions
+    assert lib.hb_band_workspace_size(1, B, L, H, D, 32, 200) == 3 * B * H * 256 * D * 4
     band = lambda ws, wsb: lib.hb_band_diffattn(None, qkv, 0, 5 * H * D, w, w, tab, tab, 32, 200, None, 0x50000,  # noqa: E731
                                                 B, L, H, D, ws, wsb)
     assert band(None, 0) == 8 and band(ws, need - 1) == 8 and band(ws + 64, need) == 8

@@ -114,6 +114,36 @@ def test_band_fp32_vs_oracle(shape):
     assert_fp32_parity(got, oracle(inp, "xla", compute="fp32"), f"fp32 {shape}")
 
 
+@pytest.mark.parametrize("shape", FP32_SHAPES[:4] + [(1, 1000, 1, 64, 100, 32)], ids=lambda s: "B%dS%dH%dD%dw%dh%d" % s)
+def test_band_fp32_without_workspace_vs_oracle(shape):
+    """The fp32 band call with a NULL workspace (each query block prepares its own key window) against the oracle
+    and against the call with a workspace (every key prepared once), through the C ABI."""
+    from hummingbird_amd import _lib
+
+    b, length, h, d, w, half = shape
+    announce(f"band fp32 without workspace {shape}")
+    inp = workloads.band_inputs(b, length, h, d, w, seed=16 + length, dtype="fp32", half=half)
+    lib = _lib.load()
+    qkv = torch.from_numpy(inp["qkv"]).to(DEV)
+    qd, kd = ba.pack_dyt(norm_t(inp["q_norm"]), d, DEV), ba.pack_dyt(norm_t(inp["k_norm"]), d, DEV)
+    cos, sin = ba.rope_tables(length, torch.from_numpy(inp["inv_freq"]).to(DEV))
+    lam = torch.from_numpy(inp["lam"]).to(DEV)
+    need = int(lib.hb_band_workspace_size(_lib.HB_F32, b, length, h, d, half, w))
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    outs = []
+    stream = torch.cuda.current_stream().cuda_stream
+    for ws_p, ws_b in ((0, 0), (ws.data_ptr(), need)):
+        out = torch.empty((b, length, h * d), dtype=torch.float32, device=DEV)
+        _lib.check(lib.hb_band_diffattn(stream, qkv.data_ptr(), _lib.HB_F32, 5 * h * d, qd.data_ptr(), kd.data_ptr(),
+                                        cos.data_ptr() if half else 0, sin.data_ptr() if half else 0, half, w,
+                                        lam.data_ptr(), out.data_ptr(), b, length, h, d, ws_p, ws_b), "band fp32")
+        outs.append(out.cpu().numpy())
+    ref = oracle(inp, "xla", compute="fp32")
+    assert_fp32_parity(outs[0], ref, f"fp32 no workspace {shape}")
+    assert_fp32_parity(outs[1], ref, f"fp32 workspace {shape}")
+    assert_fp32_parity(outs[0], outs[1], f"fp32 with vs without workspace {shape}")
+
+
 def test_band_fp32_identical_branches_cancel():
     announce("band fp32 identical branches")
     inp = workloads.band_inputs(1, 300, 2, 64, 40, seed=5, dtype="fp32")
