@@ -249,6 +249,8 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
     res["same_l_block_120s"] = block_shape(lib, sp, stream, dev, gen)
     res["dit_self_attention_120s"] = dit_self_attention_shape(stream, dev, gen)
     res["sampler_120s"] = sampler_shape(dev)
+    # the matrix cores' data dependence: what the dense kernel's roofline fraction is measured against in practice
+    res["mfma_ceiling"] = ceiling_summary(lib, sp, stream, dev)
     return res
 
 
@@ -463,9 +465,27 @@ def sweep(lib, sp, stream, dev) -> None:
 
 
 def ceiling(lib, sp, stream, dev) -> None:
-    """Throughput of the matrix cores as a function of the operand data: the vendor GEMM (torch -> hipBLASLt,
-    bf16 8192^3) and the dense call at B=2, L=2584, H=24, D=64, each with N(0,1), all-zero and all-one inputs.
-    One JSON line per case."""
+    """Throughput of the matrix cores as a function of the operand data (`ceiling_rows`), one JSON line per case."""
+    for row in ceiling_rows(lib, sp, stream, dev):
+        print(json.dumps(row), flush=True)
+
+
+def ceiling_summary(lib, sp, stream, dev) -> dict:
+    """`ceiling_rows` in short, for the default bench line: TFLOP/s at p50 per (kernel, data) and the dense kernel's
+    N(0,1) rate as a fraction of the vendor GEMM's N(0,1) rate, the practical ceiling on random operands."""
+    rows = ceiling_rows(lib, sp, stream, dev)
+    out = {f"{'gemm' if r['ceiling'].startswith('torch') else 'dense_attend'}_{r['data']}_tflops": r["tflops_p50"]
+           for r in rows}
+    out["gemm_shape"] = [8192, 8192, 8192]
+    out["dense_vs_gemm_randn"] = round(out["dense_attend_randn_tflops"] / out["gemm_randn_tflops"], 3)
+    return out
+
+
+def ceiling_rows(lib, sp, stream, dev, rounds: int = 3) -> list[dict]:
+    """The vendor GEMM (torch -> hipBLASLt, bf16 8192^3) and the dense call at B=2, L=2584, H=24, D=64, each with
+    N(0,1), all-zero and all-one inputs: per-call percentiles and TFLOP/s at p50. The six cases are interleaved
+    over `rounds` rounds and each reports the round with the median p50: the matrix cores slow down as the chip
+    heats, so cases timed one after the other would compare different power states."""
     import torch
 
     from hummingbird_amd import _lib
@@ -473,13 +493,6 @@ def ceiling(lib, sp, stream, dev) -> None:
     from hummingbird_amd import workloads as wl
 
     n = 8192
-    for kind in ("randn", "zeros", "ones"):
-        a = getattr(torch, kind)((n, n), device=dev, dtype=torch.bfloat16)
-        b = getattr(torch, kind)((n, n), device=dev, dtype=torch.bfloat16)
-        pc = call_percentiles(lambda: torch.mm(a, b), 20, stream)
-        print(json.dumps({"ceiling": "torch.mm bf16", "shape": [n, n, n], "data": kind, "us_per_call": pc,
-                          "tflops_p50": round(2 * n ** 3 / (pc["p50"] * 1e-6) / 1e12, 1)}), flush=True)
-        del a, b
     d = wl.DENSE_120S
     B, L, H, D = d["batch"], d["length"], d["heads"], d["head_dim"]
     inp = wl.dense_inputs(B, L, H, D, seed=0)
@@ -487,22 +500,36 @@ def ceiling(lib, sp, stream, dev) -> None:
     cos, sin, mask = da.tables(L, torch.from_numpy(inp["inv_freq"]).to(dev), torch.from_numpy(inp["valid"]).to(dev),
                                D, torch.bfloat16)
     wsb = int(lib.hb_dense_workspace_size(_lib.HB_BF16, B, L, H, D))
-    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     out = torch.empty((B, L, H * D), dtype=torch.bfloat16, device=dev)
+    cases = []
+    for kind in ("randn", "zeros", "ones"):
+        a = getattr(torch, kind)((n, n), device=dev, dtype=torch.bfloat16)
+        b = getattr(torch, kind)((n, n), device=dev, dtype=torch.bfloat16)
+        cases.append(({"ceiling": "torch.mm bf16", "shape": [n, n, n], "data": kind}, 2 * n ** 3, 20,
+                      lambda a=a, b=b: torch.mm(a, b)))
     for kind in ("randn", "zeros", "ones"):
         qkv = getattr(torch, kind)((B, L, 5 * H * D), device=dev, dtype=torch.bfloat16)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         _lib.check(lib.hb_dense_prep(sp, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, qw.data_ptr(), kw.data_ptr(),
                                      cos.data_ptr(), sin.data_ptr(), inp["half"], mask.data_ptr(), B, L, H, D, 1e-6,
                                      ws.data_ptr(), wsb), "prep")
-        pc = call_percentiles(lambda: _lib.check(lib.hb_dense_attend(sp, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D,
-                                                                     qw.data_ptr(), kw.data_ptr(), cos.data_ptr(),
-                                                                     sin.data_ptr(), inp["half"], 0, out.data_ptr(),
-                                                                     B, L, H, D, 1e-6, ws.data_ptr(), wsb),
-                                                 "attend"), 50, stream)
-        print(json.dumps({"ceiling": DENSE_KERNEL, "shape": [B, L, H, D], "data": kind, "us_per_call": pc,
-                          "tflops_p50": round(wl.dense_flops(B, L, H, D) / (pc["p50"] * 1e-6) / 1e12, 1)}),
-              flush=True)
-        del qkv
+
+        def attend(qkv=qkv, ws=ws):
+            _lib.check(lib.hb_dense_attend(sp, qkv.data_ptr(), _lib.HB_BF16, 5 * H * D, qw.data_ptr(), kw.data_ptr(),
+                                           cos.data_ptr(), sin.data_ptr(), inp["half"], 0, out.data_ptr(), B, L, H,
+                                           D, 1e-6, ws.data_ptr(), wsb), "attend")
+        cases.append(({"ceiling": DENSE_KERNEL, "shape": [B, L, H, D], "data": kind}, wl.dense_flops(B, L, H, D), 50,
+                      attend))
+    runs: list[list[dict]] = [[] for _ in cases]
+    for _ in range(rounds):
+        for i, (_, _, iters, fn) in enumerate(cases):
+            runs[i].append(call_percentiles(fn, iters, stream))
+    rows = []
+    for (head, flops, _, _), pcs in zip(cases, runs):
+        pc = sorted(pcs, key=lambda p: p["p50"])[len(pcs) // 2]
+        rows.append({**head, "us_per_call": pc, "tflops_p50": round(flops / (pc["p50"] * 1e-6) / 1e12, 1),
+                     "rounds": rounds})
+    return rows
 
 
 def main() -> int:
