@@ -259,7 +259,8 @@ def sampler_shape(dev) -> dict:
     24 heads; random weights), batch 1, 1358 latents + 64 memory tokens (L = 1422), a 257-token context, 8 pingpong
     steps, bf16, attention="hip" (192 dense self-attention and 192 cross-attention calls). Per-clip state from
     `dit.prepare_static` (not timed); then ms per clip for the eager loop and for the loop captured as one HIP
-    graph (median of 3 each)."""
+    graph (median of 3 each), and for the graph again after `sampling.tune_gemms` has let PyTorch's TunableOp pick
+    each GEMM's solution (the tuning itself is not timed; TunableOp is switched off again afterwards)."""
     import torch
 
     from hummingbird_amd import dit, sampling
@@ -289,12 +290,27 @@ def sampler_shape(dev) -> dict:
             torch.cuda.synchronize()
             times.append(a.elapsed_time(b))
         return round(float(np.median(times)), 2)
-    eager = clip_ms(lambda: sampling.pingpong(params, x0, schedule, noise, static, cfg, BF16, trajectory=False))
+    def eager_clip():
+        return sampling.pingpong(params, x0, schedule, noise, static, cfg, BF16, trajectory=False)
+    eager = clip_ms(eager_clip)
     graph = sampling.PingpongGraph(params, static, cfg, BF16, x0, noise)
     replay = clip_ms(lambda: graph(x0, noise))
+    del graph
+    # GEMM solutions chosen per shape by PyTorch's TunableOp (tuning untimed), then the graph captured again
+    import tempfile
+    import time
+    with tempfile.TemporaryDirectory() as tmp:
+        t0 = time.perf_counter()
+        sampling.tune_gemms(eager_clip, filename=f"{tmp}/tunableop_results.csv")
+        tune_s = time.perf_counter() - t0
+        graph = sampling.PingpongGraph(params, static, cfg, BF16, x0, noise)
+        tuned = clip_ms(lambda: graph(x0, noise))
+        del graph
+        torch.cuda.tunable.enable(False)
     return {"shape": {"B": 1, "latents": T, "L": T + cfg.num_memory_tokens, "context": 257, "depth": cfg.depth,
                       "E": cfg.embed_dim, "H": cfg.num_heads, "steps": steps},
             "eager_ms_per_clip": eager, "graph_ms_per_clip": replay,
+            "graph_ms_per_clip_tuned_gemms": tuned, "gemm_tuning_s": round(tune_s, 1),
             "attention_calls_per_clip": {"dense": steps * cfg.depth, "cross": steps * cfg.depth}}
 
 

@@ -122,3 +122,21 @@ class PingpongGraph:
         self.noise.copy_(noise)
         self.graph.replay()
         return self.out
+
+
+def tune_gemms(run: Callable[[], object], filename: str | None = None) -> None:
+    """Let PyTorch's TunableOp pick, per GEMM shape, the fastest hipBLASLt / rocBLAS solution for the GEMMs that
+    `run()` issues (the denoiser's projections and feed-forward), then keep those choices for later calls in this
+    process. Opt-in and process-wide: it enables `torch.cuda.tunable`. `filename` keeps the results for a later
+    process (`torch.cuda.tunable.read_file`). Call it before capturing a `PingpongGraph`, since capture does not
+    tune."""
+    tunable = torch.cuda.tunable
+    tunable.enable(True)
+    if filename is not None:
+        tunable.set_filename(filename)
+    tunable.tuning_enable(True)
+    try:
+        run()
+        torch.cuda.synchronize()
+    finally:
+        tunable.tuning_enable(False)

@@ -124,3 +124,34 @@ def test_sampler_graph_replays_equal_the_eager_loop(projections):
         torch.cuda.synchronize()
         assert torch.equal(got, ref), f"replay {rep}: {stats(got.float().cpu().numpy(), ref.float().cpu().numpy())}"
         _ = (torch.randn(1000, device=DEV) * 2).sum().item()  # unrelated eager work between replays
+
+
+def test_tuned_gemms_keep_parity_and_graph_replays():
+    """After sampling.tune_gemms (TunableOp picks each GEMM's solution) the medium denoiser still matches the XLA
+    chain at the contract, and a graph captured afterwards replays bit-identically to the eager loop."""
+    announce("tune_gemms: parity and graph replay")
+    params, cond, mask, x = case(MEDIUM2, BF16, 1, 200, seed=27, ctx_tokens=257)
+    static = dit.prepare_static(params, cond, mask, MEDIUM2, BF16)
+    noise = torch.randn((2, 1, MEDIUM2.io_channels, 200), generator=torch.Generator().manual_seed(28)).to(DEV)
+    schedule = sampling.build_schedule(2, device=DEV)
+
+    def eager():
+        return sampling.pingpong(params, x, schedule, noise, static, MEDIUM2, BF16, trajectory=False)[0]
+    try:
+        sampling.tune_gemms(eager)
+        assert torch.cuda.tunable.is_enabled() and not torch.cuda.tunable.tuning_is_enabled()
+        t = torch.tensor([0.7], device=DEV)
+        got = dit.dit_forward(params, x, t, static, MEDIUM2, BF16).float().cpu().numpy()
+        xcfg = dataclasses.replace(MEDIUM2, attention="xla")
+        ref = dit.dit_forward(params, x, t, dit.prepare_static(params, cond, mask, xcfg, BF16), xcfg,
+                              BF16).float().cpu().numpy()
+        scale = float(np.abs(ref).max())
+        assert_bf16_parity(got / scale, ref / scale, "tuned medium dit_forward / max")
+        graph = sampling.PingpongGraph(params, static, MEDIUM2, BF16, x, noise)
+        for _ in range(2):
+            out = graph(x, noise).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager())
+    finally:
+        torch.cuda.tunable.tuning_enable(False)
+        torch.cuda.tunable.enable(False)
