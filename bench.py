@@ -58,6 +58,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--sampler-only", action="store_true",
                     help="instead of the clip benchmark: the whole 120 s render of the medium DiT (8 pingpong steps "
                          "x 24 blocks, eager and as one HIP graph), one JSON line; for profiling under rocprofv3")
+    ap.add_argument("--no-tune", action="store_true",
+                    help="skip the sampler timing with TunableOp-selected GEMMs (whose search launches thousands of "
+                         "candidate kernels; for profiling the loop itself)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the per-kernel timing loops plus one 256 MiB device copy (the traffic-counter "
                          "calibration kernel); for profiling under rocprofv3")
@@ -254,7 +257,7 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
     return res
 
 
-def sampler_shape(dev) -> dict:
+def sampler_shape(dev, tune: bool = True) -> dict:
     """The whole denoising of one 120 s clip as the reference renders it: the `medium` DiT (24 blocks, width 1536,
     24 heads; random weights), batch 1, 1358 latents + 64 memory tokens (L = 1422), a 257-token context, 8 pingpong
     steps, bf16, attention="hip" (192 dense self-attention and 192 cross-attention calls). Per-clip state from
@@ -296,6 +299,12 @@ def sampler_shape(dev) -> dict:
     graph = sampling.PingpongGraph(params, static, cfg, BF16, x0, noise)
     replay = clip_ms(lambda: graph(x0, noise))
     del graph
+    shape = {"B": 1, "latents": T, "L": T + cfg.num_memory_tokens, "context": 257, "depth": cfg.depth,
+             "E": cfg.embed_dim, "H": cfg.num_heads, "steps": steps}
+    calls = {"dense": steps * cfg.depth, "cross": steps * cfg.depth}
+    if not tune:
+        return {"shape": shape, "eager_ms_per_clip": eager, "graph_ms_per_clip": replay,
+                "attention_calls_per_clip": calls}
     # GEMM solutions chosen per shape by PyTorch's TunableOp (tuning untimed), then the graph captured again
     import tempfile
     import time
@@ -307,11 +316,9 @@ def sampler_shape(dev) -> dict:
         tuned = clip_ms(lambda: graph(x0, noise))
         del graph
         torch.cuda.tunable.enable(False)
-    return {"shape": {"B": 1, "latents": T, "L": T + cfg.num_memory_tokens, "context": 257, "depth": cfg.depth,
-                      "E": cfg.embed_dim, "H": cfg.num_heads, "steps": steps},
-            "eager_ms_per_clip": eager, "graph_ms_per_clip": replay,
+    return {"shape": shape, "eager_ms_per_clip": eager, "graph_ms_per_clip": replay,
             "graph_ms_per_clip_tuned_gemms": tuned, "gemm_tuning_s": round(tune_s, 1),
-            "attention_calls_per_clip": {"dense": steps * cfg.depth, "cross": steps * cfg.depth}}
+            "attention_calls_per_clip": calls}
 
 
 def dit_self_attention_shape(stream, dev, gen) -> dict:
@@ -574,7 +581,7 @@ def main() -> int:
         ceiling(lib, sp, stream, dev)
         return 0
     if args.sampler_only:
-        print(json.dumps({"sampler_120s": sampler_shape(dev)}), flush=True)
+        print(json.dumps({"sampler_120s": sampler_shape(dev, tune=not args.no_tune)}), flush=True)
         return 0
 
     # ---- dense inputs (two qkv buffers alternate, as consecutive blocks would) ----

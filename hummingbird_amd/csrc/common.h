@@ -51,9 +51,17 @@ struct F16Io {
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(h[i]);
   }
-  // IEEE half round to nearest even (v_cvt_f16_f32 in the default rounding mode)
-  __device__ static __forceinline__ float round(float f) { return static_cast<float>(static_cast<_Float16>(f)); }
+  // IEEE half round to nearest even (v_cvt_f16_f32 in the default rounding mode) of an fp32 value. The empty asm
+  // makes the fp32 value exist before the conversion: otherwise the compiler may fold the multiply or subtract
+  // that produced it into a mixed-precision FMA (v_fma_mixlo_f16), which rounds the exact result to half once,
+  // where the source (and the reference's fp32 arithmetic followed by a cast) rounds to fp32 first. The two differ
+  // by one half step when the fp32 result lies exactly on a half-precision tie.
+  __device__ static __forceinline__ float round(float f) {
+    asm volatile("" : "+v"(f));
+    return static_cast<float>(static_cast<_Float16>(f));
+  }
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    asm volatile("" : "+v"(lo), "+v"(hi));
     f16x2 h;
     h[0] = static_cast<_Float16>(lo);
     h[1] = static_cast<_Float16>(hi);

@@ -167,41 +167,45 @@ __global__ __launch_bounds__(256) void residual_rms_kernel(
   if (n >= N) return;  // wave-uniform
   const int64_t b = n / L;
   const bool latent = static_cast<int>(n - b * L) >= memory;
-  float r[KMAX][V];
+  // Every load of the row first (chunks past C are not read), so the wave waits for memory once.
+  float r[KMAX][V], xv[KMAX][V], g[KMAX][V], bv[KMAX][V], lv[KMAX][V];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int c0 = (lane + 64 * k) * V;
+    if (c0 < C) {
+      Vec<T>::load(h + n * hs + c0, r[k]);
+      Vec<T>::load(x + n * xs + c0, xv[k]);
+      if (xbias) Vec<T>::load(xbias + c0, bv[k]);
+      if (gate) Vec<T>::load(gate + b * gate_stride + c0, g[k]);
+      if (local && latent) Vec<T>::load(local + c0, lv[k]);
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int c0 = (lane + 64 * k) * V;
-    if (c0 >= C) break;
-    float xv[V];
-    Vec<T>::load(h + n * hs + c0, r[k]);
-    Vec<T>::load(x + n * xs + c0, xv);
-    if (xbias) {
-      float bv[V];
-      Vec<T>::load(xbias + c0, bv);
+    if (c0 < C) {
+      if (xbias) {
 #pragma unroll
-      for (int j = 0; j < V; ++j) xv[j] = Vec<T>::round(xv[j] + bv[j]);
-    }
-    if (gate) {
-      float g[V];
-      Vec<T>::load(gate + b * gate_stride + c0, g);
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const float u = Vec<T>::round(1.f - g[j]);
-        xv[j] = Vec<T>::round(xv[j] * Vec<T>::round(1.f / (1.f + expf(-u))));
+        for (int j = 0; j < V; ++j) xv[k][j] = Vec<T>::round(xv[k][j] + bv[k][j]);
       }
+      if (gate) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const float u = Vec<T>::round(1.f - g[k][j]);
+          xv[k][j] = Vec<T>::round(xv[k][j] * Vec<T>::round(1.f / (1.f + expf(-u))));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < V; ++j) r[k][j] = Vec<T>::round(r[k][j] + xv[k][j]);
+      if (local && latent) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) r[k][j] = Vec<T>::round(r[k][j] + lv[k][j]);
+      }
+      Vec<T>::store(out_h + n * os + c0, r[k]);
+#pragma unroll
+      for (int j = 0; j < V; ++j) ss = ss + r[k][j] * r[k][j];
     }
-#pragma unroll
-    for (int j = 0; j < V; ++j) r[k][j] = Vec<T>::round(r[k][j] + xv[j]);
-    if (local && latent) {
-      float lv[V];
-      Vec<T>::load(local + c0, lv);
-#pragma unroll
-      for (int j = 0; j < V; ++j) r[k][j] = Vec<T>::round(r[k][j] + lv[j]);
-    }
-    Vec<T>::store(out_h + n * os + c0, r[k]);
-#pragma unroll
-    for (int j = 0; j < V; ++j) ss = ss + r[k][j] * r[k][j];
   }
   const float inv = rsqrtf(wave_sum(ss) * (1.f / static_cast<float>(C)) + eps);
   const T* sc = scale ? scale + b * mod_stride : nullptr;
@@ -209,18 +213,19 @@ __global__ __launch_bounds__(256) void residual_rms_kernel(
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int c0 = (lane + 64 * k) * V;
-    if (c0 >= C) break;
-    float v[V];
+    if (c0 < C) {
+      float v[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) v[j] = Vec<T>::round((r[k][j] * inv) * w[c0 + j]);
-    if (sc) {
-      float s[V], t[V];
-      Vec<T>::load(sc + c0, s);
-      Vec<T>::load(sh + c0, t);
+      for (int j = 0; j < V; ++j) v[j] = Vec<T>::round((r[k][j] * inv) * w[c0 + j]);
+      if (sc) {
+        float s[V], t[V];
+        Vec<T>::load(sc + c0, s);
+        Vec<T>::load(sh + c0, t);
 #pragma unroll
-      for (int j = 0; j < V; ++j) v[j] = Vec<T>::round(Vec<T>::round(v[j] * Vec<T>::round(1.f + s[j])) + t[j]);
+        for (int j = 0; j < V; ++j) v[j] = Vec<T>::round(Vec<T>::round(v[j] * Vec<T>::round(1.f + s[j])) + t[j]);
+      }
+      Vec<T>::store(out_y + n * os + c0, v);
     }
-    Vec<T>::store(out_y + n * os + c0, v);
   }
 }
 
