@@ -6,7 +6,7 @@ done with torch's bf16 / fp16 conversion (a library routine, not the oracle's). 
 each cast point's plausible mistake (the rounding dropped, or added where the reference keeps fp32) into the
 oracle and check that one of these pins fails.
 
-Cast points:
+Cast points (where the reference rounds to the compute dtype on each chain):
   XLA dense chain (oracle.dense.dense_xla / sdpa): RMSNorm cast (dit.py:57), RoPE cast (dit.py:98), bf16 logits
   (dit.py:117), the scale multiply in bf16 (dit.py:117), bf16 weights (dit.py:118), bf16 P @ V (dit.py:119), bf16
   subtraction (dit.py:146).
