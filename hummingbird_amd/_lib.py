@@ -58,6 +58,8 @@ SIGNATURES = {
                                 c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t]),
     "hb_dyt": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int]),
     "hb_glu": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int, c_void_p, c_int64, c_int64, c_int]),
+    "hb_residual_dyt": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
+                                c_void_p, c_int64, c_int64, c_int]),
     "hb_rms_modulate": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_float, c_void_p, c_void_p, c_int64,
                                 c_int, c_void_p, c_int64, c_int64, c_int]),
     "hb_gated_residual": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,

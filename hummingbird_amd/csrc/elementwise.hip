@@ -129,6 +129,44 @@ __global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ proj, in
   }
 }
 
+// The block's residual adds with what surrounds them (same_l.py:191-192): out_h = h + (x + bias), the projection's
+// bias added first (same_l._linear: the matmul, then the bias add) and each sum held in the compute dtype; then,
+// with `dyt`, out_y = cast(DyT(out_h)), the input of the next GEMM (ff_norm inside the block, or the next block's
+// pre_norm). One pass where the XLA chain makes two or three. `bias` (C values of the compute dtype as fp32) and
+// `dyt` (packed as for dyt_kernel) may be null; out_h may be h itself.
+template <typename T>
+__global__ __launch_bounds__(256) void residual_dyt_kernel(const T* h, int64_t hs, const T* __restrict__ x,
+                                                           int64_t xs, const float* __restrict__ bias,
+                                                           const float* __restrict__ dyt, T* out_h,
+                                                           T* __restrict__ out_y, int64_t os, int64_t N, int C) {
+  constexpr int V = Vec<T>::N;
+  const int chunks = C / V;
+  const float a2 = dyt ? 2.f * kLog2e * dyt[0] : 0.f;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < N * chunks;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t n = i / chunks;
+    const int c0 = static_cast<int>(i - n * chunks) * V;
+    float hv[V], xv[V];
+    Vec<T>::load(h + n * hs + c0, hv);
+    Vec<T>::load(x + n * xs + c0, xv);
+    if (bias) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) xv[j] = Vec<T>::round(xv[j] + bias[c0 + j]);
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) hv[j] = Vec<T>::round(hv[j] + xv[j]);
+    Vec<T>::store(out_h + n * os + c0, hv);
+    if (dyt) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float g = dyt[1 + c0 + j], b = dyt[1 + C + c0 + j];
+        hv[j] = dyt_tanh(hv[j], a2, -2.f * g, g + b);
+      }
+      Vec<T>::store(out_y + n * os + c0, hv);  // the store's conversion is the single cast
+    }
+  }
+}
+
 }  // namespace ew
 }  // namespace hb
 
@@ -226,6 +264,37 @@ int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_str
                          o, out_row_stride, N, F);
   }
   return launched("glu");
+}
+
+int hb_residual_dyt(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* x,
+                    int64_t x_row_stride, const float* bias, const float* dyt, void* out_h, void* out_y,
+                    int64_t out_row_stride, int64_t N, int C) {
+  clear_error();
+  int st = check_rows("residual_dyt", dtype, h, h_row_stride, out_h, out_row_stride, N, C, C);
+  if (st) return st;
+  st = check_rows("residual_dyt", dtype, x, x_row_stride, out_h, out_row_stride, N, C, C);
+  if (st) return st;
+  if (!dyt != !out_y) return fail(HB_ERR_NULL, "residual_dyt: dyt and out_y are given together or not at all");
+  if (out_y && reinterpret_cast<uintptr_t>(out_y) % 16)
+    return fail(HB_ERR_STRIDE, "residual_dyt: out_y must be 16-byte aligned");
+  if (out_y && (out_y == h || out_y == x || out_y == out_h))
+    return fail(HB_ERR_STRIDE, "residual_dyt: out_y must not alias h, x or out_h");
+  if (out_h == x || (out_h == h && h_row_stride != out_row_stride))
+    return fail(HB_ERR_STRIDE, "residual_dyt: out_h may alias h (with the same row stride) but not x");
+  const dim3 grid = row_grid(N, C / (dtype == HB_F32 ? 4 : 8));
+  if (dtype == HB_BF16)
+    hipLaunchKernelGGL(ew::residual_dyt_kernel<uint16_t>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(h),
+                       h_row_stride, static_cast<const uint16_t*>(x), x_row_stride, bias, dyt,
+                       static_cast<uint16_t*>(out_h), static_cast<uint16_t*>(out_y), out_row_stride, N, C);
+  else if (dtype == HB_F16)
+    hipLaunchKernelGGL(ew::residual_dyt_kernel<_Float16>, grid, dim3(256), 0, stream, static_cast<const _Float16*>(h),
+                       h_row_stride, static_cast<const _Float16*>(x), x_row_stride, bias, dyt,
+                       static_cast<_Float16*>(out_h), static_cast<_Float16*>(out_y), out_row_stride, N, C);
+  else
+    hipLaunchKernelGGL(ew::residual_dyt_kernel<float>, grid, dim3(256), 0, stream, static_cast<const float*>(h),
+                       h_row_stride, static_cast<const float*>(x), x_row_stride, bias, dyt,
+                       static_cast<float*>(out_h), static_cast<float*>(out_y), out_row_stride, N, C);
+  return launched("residual_dyt");
 }
 
 }  // extern "C"

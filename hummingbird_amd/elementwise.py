@@ -70,6 +70,35 @@ def glu(proj: torch.Tensor, sinusoidal: bool, bias: torch.Tensor | None = None) 
     return out
 
 
+def residual_dyt(h: torch.Tensor, x: torch.Tensor, bias: torch.Tensor | None = None,
+                 norm: dict | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """`(h + (x + bias), cast(DyT(h + (x + bias))))` in one pass: a residual add of the SAME-L block (reference:
+    same_l._block, same_l.py:191-192) after the projection's bias add (same_l._linear), each sum held in the compute
+    dtype, and with `norm` (DyT params) the DyT of the sum cast back, the next GEMM's input. `x` is the bare
+    projection output; `bias` (C values) may be None. Without `norm` the second result is None."""
+    _require_gpu(h, "h")
+    if h.shape != x.shape or h.dtype != x.dtype:
+        raise ValueError(f"h {tuple(h.shape)} {h.dtype} and x {tuple(x.shape)} {x.dtype} must match")
+    channels = h.shape[-1]
+    rows, hs = _rows(h, "h")
+    _, xs = _rows(x, "x")
+    bias_p = 0
+    if bias is not None:
+        bias = bias.to(device=h.device, dtype=torch.float32).contiguous().reshape(-1)
+        if bias.numel() != channels:
+            raise ValueError(f"bias must have {channels} elements")
+        bias_p = bias.data_ptr()
+    params = pack_dyt(norm, channels, h.device) if norm is not None else None
+    out_h = torch.empty(h.shape, dtype=h.dtype, device=h.device)
+    out_y = torch.empty(h.shape, dtype=h.dtype, device=h.device) if norm is not None else None
+    stream = torch.cuda.current_stream(h.device).cuda_stream
+    _lib.check(_lib.load().hb_residual_dyt(stream, h.data_ptr(), dtype_code(h.dtype), hs, x.data_ptr(), xs, bias_p,
+                                           params.data_ptr() if params is not None else 0, out_h.data_ptr(),
+                                           out_y.data_ptr() if out_y is not None else 0, channels, rows, channels),
+               "residual_dyt")
+    return out_h, out_y
+
+
 def _per_batch(t: torch.Tensor | None, batch: int, channels: int, dtype: torch.dtype, name: str):
     """(pointer, batch stride) of a `(B, C)` (or `(B, 1, C)`) per-batch row tensor in `dtype`, possibly a view into a
     wider row (the adaLN chunks of `(B, 6 E)`); (0, 0) for None."""

@@ -1,8 +1,9 @@
 """The SAME-L decoder block with the `attention="hip"` dispatch: its attention step (sa3jax/same_l.py:151-169),
 its feed-forward (sa3jax/same_l.py:172-183) and the block around them (sa3jax/same_l.py:186-192).
 
-`attention="hip"` runs the band attention, the two DyT norms and the GLU gate as HIP kernels and the projections
-as torch GEMMs (hipBLASLt); `attention="xla"` runs the torch restatement of the reference's chain.
+`attention="hip"` runs the band attention, the DyT norms, the GLU gate and the residual adds (fused with the DyT or
+the bias add next to them) as HIP kernels and the projections as torch GEMMs (hipBLASLt); `attention="xla"` runs
+the torch restatement of the reference's chain.
 """
 from __future__ import annotations
 
@@ -65,6 +66,14 @@ def block(x: torch.Tensor, params: dict, index: int, cfg: SameConfig,
     `h = x + attention(DyT(x; pre_norm))`, then `h + feed_forward(DyT(h; ff_norm))`, each DyT in fp32 and cast
     back to `x.dtype` before its GEMM. `params` holds `pre_norm`, `ff_norm` (DyT params), `self_attn`,
     `rope_inv_freq` (as `attention` reads them) and `ff.{glu_proj,proj_out}.{weight,bias}`."""
-    norm = elementwise.dyt if use_hip(cfg, x) else xla_chain.dyt_cast
-    h = x + attention(norm(x, params["pre_norm"]), params, cfg, lam=lam)
-    return h + feed_forward(norm(h, params["ff_norm"]), params, index, cfg)
+    if not use_hip(cfg, x):
+        h = x + attention(xla_chain.dyt_cast(x, params["pre_norm"]), params, cfg, lam=lam)
+        return h + feed_forward(xla_chain.dyt_cast(h, params["ff_norm"]), params, index, cfg)
+    # The residual adds run fused with what surrounds them, with the same roundings: the first with the ff_norm DyT
+    # that follows it, the second with proj_out's bias add before it.
+    a = attention(elementwise.dyt(x, params["pre_norm"]), params, cfg, lam=lam)
+    h, y = elementwise.residual_dyt(x, a, norm=params["ff_norm"])
+    ff = params["ff"]
+    gated = elementwise.glu(y @ ff["glu_proj"]["weight"].t(), cfg.sinusoidal(index), bias=ff["glu_proj"].get("bias"))
+    out, _ = elementwise.residual_dyt(h, gated @ ff["proj_out"]["weight"].t(), bias=ff["proj_out"].get("bias"))
+    return out

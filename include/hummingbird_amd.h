@@ -9,8 +9,8 @@
  *                      called from same_l._attention (sa3jax/same_l.py:158-161);
  *   hb_cross_prep +    replace   the XLA chain of dit._cross_attention and its hoisted context K/V
  *   hb_cross_attend              (sa3jax/dit.py:203-215, 274-284), which the reference runs without a kernel;
- *   hb_dyt, hb_glu     replace   the elementwise steps of same_l._block around its GEMMs (sa3jax/same_l.py:58-69,
- *                                172-192), an XLA chain in the reference;
+ *   hb_dyt, hb_glu,    replace   the elementwise steps of same_l._block around its GEMMs (sa3jax/same_l.py:58-69,
+ *   hb_residual_dyt              172-192), an XLA chain in the reference;
  *   hb_dit_qkv_proj,   replace   the GEMMs either side of the DiT kernel (sa3jax/dit.py:190, 195), the first with the
  *   hb_dense_attend_qq,          dense kernel's key preparation in its epilogue;
  *   hb_proj
@@ -223,6 +223,17 @@ int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, c
            int64_t out_row_stride, int64_t N, int C);
 int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_stride, const float* bias,
            int sinusoidal, void* out, int64_t out_row_stride, int64_t N, int F);
+
+/*   hb_residual_dyt : out_h = h + (x + bias), the residual adds of same_l._block (sa3jax/same_l.py:191, 192) after
+ *                     the projection's bias add (same_l._linear), each sum rounded to the compute dtype; `bias` (C
+ *                     floats holding values of the compute dtype) may be NULL. With `dyt` (packed as for hb_dyt) also
+ *                     out_y = cast(DyT(out_h)), the input of the next GEMM (ff_norm, or the next block's pre_norm);
+ *                     `dyt` and `out_y` are both given or both NULL. out_h may be h itself (same row stride); out_y
+ *                     aliases nothing. out_h and out_y share `out_row_stride`. One pass where the XLA chain makes two or
+ *                     three. */
+int hb_residual_dyt(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* x,
+                    int64_t x_row_stride, const float* bias, const float* dyt, void* out_h, void* out_y,
+                    int64_t out_row_stride, int64_t N, int C);
 
 /* ---- DiT block: the elementwise steps around the GEMMs and attention calls ---------------------------------
  * Replace the array operations of dit._block between its matmuls (sa3jax/dit.py:224-251).

@@ -213,3 +213,21 @@ def test_residual_rms_rejects_before_any_launch(lib):
     assert call(w=None) == 1 and call(scale=fake) == 1 and call(oh=None) == 1
     assert call(gate=fake, N=25) == 2         # not a whole number of batches
     assert call(dtype=4) == 3
+
+
+def test_residual_dyt_rejects_before_any_launch(lib):
+    """hb_residual_dyt checks dtype, shapes, strides, alignment, the dyt / out_y pairing and which buffers may alias
+    on the host (fake, never dereferenced addresses)."""
+    fake, other, third = 0x100000, 0x200000, 0x300000
+    call = lambda **kw: lib.hb_residual_dyt(  # noqa: E731
+        None, kw.get("h", fake), kw.get("dtype", 0), kw.get("hs", 64), kw.get("x", other), kw.get("xs", 64),
+        kw.get("bias", None), kw.get("dyt", None), kw.get("oh", fake), kw.get("oy", None), kw.get("os", 64),
+        kw.get("N", 20), kw.get("C", 64))
+    assert call(dtype=7) == 3 and call(C=60) == 2 and call(N=0) == 2
+    assert call(h=None) == 1 and call(x=None) == 1 and call(oh=None) == 1
+    assert call(xs=56) == 7 and call(x=other + 8) == 7 and call(dtype=1, C=62) == 2
+    assert call(dyt=third) == 1 and call(oy=third) == 1              # dyt and out_y come together
+    assert call(dyt=third, oy=third + 8) == 7                         # out_y 16-byte aligned
+    assert call(dyt=third, oy=other) == 7                             # out_y aliases x
+    assert call(oh=other) == 7                                        # out_h aliases x
+    assert call(os=128) == 7                                          # out_h is h with another row stride

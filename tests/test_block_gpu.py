@@ -1,7 +1,8 @@
 """GPU parity of the SAME-L block's elementwise kernels (hb_dyt, hb_glu) and of the block mirror with
 `attention="hip"`.
 
-hb_dyt and hb_glu run against the oracle: fp32 within 1e-5 relative; bf16 within one bf16 step of the oracle's
+hb_dyt and hb_glu run against the oracle; hb_residual_dyt against the torch additions it fuses (bit-identical:
+the same roundings) followed by hb_dyt (bit-identical: the same DyT code). fp32 within 1e-5 relative; bf16 within one bf16 step of the oracle's
 value on every element (the kernels' tanh, exp and sine are not bit-identical to NumPy's, so a value that lands
 next to a rounding boundary may round the other way), plus for the DyT a few fp32 units of its operands' scale
 (where gamma * tanh(alpha x) nearly cancels beta, both evaluations carry that absolute error in a tiny result),
@@ -155,3 +156,44 @@ def test_block_hip_vs_xla_and_oracle(index, dtype):
     ref = oblock.block_xla(xt.float().cpu().numpy(), rounded(p, dtype), 2, 64, CFG.sub_chunk_size,
                            CFG.sinusoidal(index), None, dtype)
     check(outs["hip"] / scale, ref / scale, f"block {index} hip vs oracle (/{scale:.3g})")
+
+
+@pytest.mark.parametrize("with_bias", [False, True], ids=["no_bias", "bias"])
+@pytest.mark.parametrize("with_dyt", [False, True], ids=["no_dyt", "dyt"])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
+def test_residual_dyt_equals_the_ops_it_fuses(dtype, with_dyt, with_bias):
+    """out_h = h + (x + bias) equals torch's additions in the compute dtype (each sum rounded once, as the reference
+    holds them) bit for bit, and out_y equals hb_dyt of out_h bit for bit, on a row slice of a wider tensor."""
+    announce(f"residual_dyt {dtype} dyt={with_dyt} bias={with_bias}")
+    tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
+    c = 512
+    h = dev(2 * RNG.standard_normal((3, 333, c)), tdt)
+    x = dev(RNG.standard_normal((3, 333, c + 64)), tdt)[..., :c]
+    bias = dev(0.1 * RNG.standard_normal(c), tdt) if with_bias else None
+    norm = ({"alpha": torch.tensor(0.7, device=DEV), "gamma": dev(1 + 0.1 * RNG.standard_normal(c)),
+             "beta": dev(0.1 * RNG.standard_normal(c))} if with_dyt else None)
+    out_h, out_y = elementwise.residual_dyt(h, x, bias=bias, norm=norm)
+    ref_h = h + ((x + bias) if with_bias else x)
+    assert ref_h.dtype == tdt and torch.equal(out_h, ref_h)
+    if with_dyt:
+        assert torch.equal(out_y, elementwise.dyt(ref_h, norm))
+    else:
+        assert out_y is None
+
+
+def test_residual_dyt_in_place():
+    """The C ABI allows out_h to be h itself: the sum lands where h was, and out_y is unchanged by the aliasing."""
+    announce("residual_dyt in place")
+    from hummingbird_amd import _lib
+    c = 256
+    h = dev(RNG.standard_normal((100, c)), torch.bfloat16)
+    x = dev(RNG.standard_normal((100, c)), torch.bfloat16)
+    norm = {"alpha": torch.tensor(0.5, device=DEV), "gamma": dev(np.ones(c)), "beta": dev(np.zeros(c))}
+    ref_h, ref_y = elementwise.residual_dyt(h, x, norm=norm)
+    params = elementwise.pack_dyt(norm, c, h.device)
+    y = torch.empty_like(h)
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(_lib.load().hb_residual_dyt(stream, h.data_ptr(), _lib.HB_BF16, c, x.data_ptr(), c, 0, params.data_ptr(),
+                                           h.data_ptr(), y.data_ptr(), c, 100, c), "residual_dyt")
+    torch.cuda.synchronize()
+    assert torch.equal(h, ref_h) and torch.equal(y, ref_y)
