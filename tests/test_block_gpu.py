@@ -197,3 +197,32 @@ def test_residual_dyt_in_place():
                                            h.data_ptr(), y.data_ptr(), c, 100, c), "residual_dyt")
     torch.cuda.synchronize()
     assert torch.equal(h, ref_h) and torch.equal(y, ref_y)
+
+
+def test_block_graph_replays_equal_eager():
+    """The whole SAME-L block with attention="hip" (hb_dyt, the band kernel, hb_glu, hb_residual_dyt and the torch
+    GEMMs) captured as one HIP graph: three replays with new inputs, eager work in between, each bit-identical to
+    the eager block on the same input."""
+    announce("same-l block graph replays")
+    cfg = SameConfig(channels=64, c_mults=(2,), stride=16, transformer_depth=4, sinusoidal_blocks=2, attention="hip")
+    p = to_torch(block_params(128, 2, 384, seed=60), DEV, torch.bfloat16)
+    static_x = dev(RNG.standard_normal((1, 700, 128)), torch.bfloat16)
+    same_l.block(static_x, p, 3, cfg)  # warm-up: table caches, library load
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        same_l.block(static_x, p, 3, cfg)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = same_l.block(static_x, p, 3, cfg)
+    for replay in range(3):
+        x = dev(RNG.standard_normal((1, 700, 128)), torch.bfloat16)
+        static_x.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = same_l.block(x, p, 3, cfg)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, ref), f"replay {replay}"
+        _ = (torch.randn(1 << 16, device=DEV) * 2).sum().item()  # unrelated eager work between replays
