@@ -16,6 +16,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import itertools
 import json
 import os
@@ -250,6 +251,7 @@ def extra_shapes(lib, sp, stream, dev) -> dict:
                          "ms_per_clip": round(wl.DENSE_CALLS_PER_CLIP * pc["p50"] / 1e3, 3)}
     del q, kv, ws, out
     res["same_l_block_120s"] = block_shape(lib, sp, stream, dev, gen)
+    res["same_l_decoder_120s"] = decoder_shape(dev, gen)
     res["dit_self_attention_120s"] = dit_self_attention_shape(stream, dev, gen)
     res["sampler_120s"] = sampler_shape(dev)
     # the matrix cores' data dependence: what the dense kernel's roofline fraction is measured against in practice
@@ -398,6 +400,69 @@ def block_shape(lib, sp, stream, dev, gen) -> dict:
             "dyt_us_per_call": pd, "dyt_hbm_frac_p50": round(dyt_bytes / (pd["p50"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "glu_us_per_call": pg, "glu_hbm_frac_p50": round(glu_bytes / (pg["p50"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "block_us_per_call": pb}
+
+
+def decoder_shape(dev, gen) -> dict:
+    """The SAME-L decoder's 12 blocks for a 120 s clip at the reference's medium geometry (1358 latents x 17 = 23086
+    frames, dim 1536 = 24 heads of 64, ff 4608, half-width 17, the last 8 blocks with the sine gate; random weights,
+    bf16): ms per clip for the chained loop (`same_l.blocks`, each block handing the next its pre_norm DyT) and for
+    the block-by-block loop, medians of 3 after one warm-up. The reference's published figure for its whole decode
+    (these blocks plus the bottleneck, token interleave and output mapping) is 61 ms on a TPU v6e-1."""
+    import torch
+
+    from hummingbird_amd import same_l
+    from hummingbird_amd import workloads as wl
+    from hummingbird_amd.config import MEDIUM_SAME_L
+
+    cfg = dataclasses.replace(MEDIUM_SAME_L, attention="hip")
+    latents = 1358
+    S, dim, ff = latents * cfg.sub_chunk_size, cfg.dim, cfg.ff_inner
+
+    def w(o, i):
+        return (torch.randn((o, i), device=dev, generator=gen) / i ** 0.5).to(torch.bfloat16)
+
+    def norm(c):
+        return {"alpha": torch.tensor(0.5, device=dev), "gamma": torch.ones(c, device=dev),
+                "beta": torch.zeros(c, device=dev)}
+
+    def zeros(n):
+        return torch.zeros(n, device=dev, dtype=torch.bfloat16)
+    inv_freq = torch.from_numpy(wl.inv_freq(16)).to(dev)
+    params = [{"pre_norm": norm(dim), "ff_norm": norm(dim), "rope_inv_freq": inv_freq,
+               "self_attn": {"to_qkv": {"weight": w(5 * dim, dim)}, "to_out": {"weight": w(dim, dim)},
+                             "q_norm": norm(64), "k_norm": norm(64)},
+               "ff": {"glu_proj": {"weight": w(2 * ff, dim), "bias": zeros(2 * ff)},
+                      "proj_out": {"weight": w(dim, ff), "bias": zeros(dim)}}}
+              for _ in range(cfg.transformer_depth)]
+    x = torch.randn((1, S, dim), device=dev, generator=gen).to(torch.bfloat16)
+
+    def chained():
+        return same_l.blocks(x, params, cfg)
+
+    def one_by_one():
+        h = x
+        for i, p in enumerate(params):
+            h = same_l.block(h, p, i, cfg)
+        return h
+
+    def ms(fn, n=3) -> float:
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(n):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        return round(float(np.median(ts)), 3)
+    res = {"shape": {"S": S, "dim": dim, "heads": cfg.num_heads, "ff": ff, "w": cfg.sub_chunk_size,
+                     "blocks": cfg.transformer_depth, "sine_blocks": cfg.sinusoidal_blocks},
+           "chained_ms_per_clip": ms(chained), "block_by_block_ms_per_clip": ms(one_by_one),
+           "reference_whole_decode_ms_tpu_v6e": 61.0}
+    del params
+    return res
 
 
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA

@@ -1,5 +1,6 @@
 """The SAME-L decoder block with the `attention="hip"` dispatch: its attention step (sa3jax/same_l.py:151-169),
-its feed-forward (sa3jax/same_l.py:172-183) and the block around them (sa3jax/same_l.py:186-192).
+its feed-forward (sa3jax/same_l.py:172-183), the block around them (sa3jax/same_l.py:186-192) and the decoder's
+loop over its blocks (sa3jax/same_l.py:236-237).
 
 `attention="hip"` runs the band attention, the DyT norms, the GLU gate and the residual adds (fused with the DyT or
 the bias add next to them) as HIP kernels and the projections as torch GEMMs (hipBLASLt); `attention="xla"` runs
@@ -69,11 +70,34 @@ def block(x: torch.Tensor, params: dict, index: int, cfg: SameConfig,
     if not use_hip(cfg, x):
         h = x + attention(xla_chain.dyt_cast(x, params["pre_norm"]), params, cfg, lam=lam)
         return h + feed_forward(xla_chain.dyt_cast(h, params["ff_norm"]), params, index, cfg)
-    # The residual adds run fused with what surrounds them, with the same roundings: the first with the ff_norm DyT
-    # that follows it, the second with proj_out's bias add before it.
-    a = attention(elementwise.dyt(x, params["pre_norm"]), params, cfg, lam=lam)
+    out, _ = _block_hip(x, elementwise.dyt(x, params["pre_norm"]), params, index, cfg, lam, None)
+    return out
+
+
+def _block_hip(x: torch.Tensor, y: torch.Tensor, params: dict, index: int, cfg: SameConfig,
+               lam: torch.Tensor | None, next_norm: dict | None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """A block from its input `x` and `y` = DyT(x; pre_norm) cast: `(out, DyT(out; next_norm) or None)`. The residual
+    adds run fused with what surrounds them, with the same roundings: the first with the ff_norm DyT that follows it,
+    the second with proj_out's bias add before it and, given `next_norm`, the next block's pre_norm DyT after it."""
+    a = attention(y, params, cfg, lam=lam)
     h, y = elementwise.residual_dyt(x, a, norm=params["ff_norm"])
     ff = params["ff"]
     gated = elementwise.glu(y @ ff["glu_proj"]["weight"].t(), cfg.sinusoidal(index), bias=ff["glu_proj"].get("bias"))
-    out, _ = elementwise.residual_dyt(h, gated @ ff["proj_out"]["weight"].t(), bias=ff["proj_out"].get("bias"))
-    return out
+    return elementwise.residual_dyt(h, gated @ ff["proj_out"]["weight"].t(), bias=ff["proj_out"].get("bias"),
+                                    norm=next_norm)
+
+
+def blocks(x: torch.Tensor, params: list, cfg: SameConfig, lam: torch.Tensor | None = None) -> torch.Tensor:
+    """The decoder's block loop (reference: same_l.decode, `for index, block in enumerate(params["blocks"])`,
+    same_l.py:236-237): `block` over `params` in order. With `attention="hip"` each block hands the next one its
+    pre_norm DyT from the pass that finishes its own residual, so a chain of n blocks makes one DyT pass instead of
+    n; the values are those of the block-by-block loop."""
+    if not use_hip(cfg, x):
+        for index, p in enumerate(params):
+            x = block(x, p, index, cfg, lam=lam)
+        return x
+    y = elementwise.dyt(x, params[0]["pre_norm"])
+    for index, p in enumerate(params):
+        nxt = params[index + 1]["pre_norm"] if index + 1 < len(params) else None
+        x, y = _block_hip(x, y, p, index, cfg, lam, nxt)
+    return x

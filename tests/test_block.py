@@ -111,6 +111,22 @@ def test_torch_chain_block_matches_oracle(compute):
                                                                           f"block {index} {compute}")
 
 
+def test_blocks_chain_matches_oracle_chain():
+    """same_l.blocks (attention="xla", fp32) over four blocks against the oracle's block applied four times: the
+    loop runs the blocks in order with their own index (the sine gate from block index 3 on)."""
+    dim, heads, ff = 128, 2, 384
+    cfg = SameConfig(channels=64, c_mults=(2,), stride=16, transformer_depth=4, sinusoidal_blocks=2,
+                     attention="xla")
+    ps = [block_params(dim, heads, ff, seed=9 + i) for i in range(4)]
+    x = RNG.standard_normal((1, 60, dim)).astype(np.float32)
+    got = same_l.blocks(torch.from_numpy(x), [to_torch(p) for p in ps], cfg).numpy()
+    ref = x
+    for i, p in enumerate(ps):
+        ref = oblock.block_xla(ref, p, heads, 64, cfg.sub_chunk_size, cfg.sinusoidal(i), None, "fp32")
+    scale = max(1.0, float(np.abs(ref).max()))
+    assert_fp32_parity(got / scale, ref / scale, "4 blocks fp32")
+
+
 # ---- the C ABI's host-side checks ---------------------------------------------------------------------------
 @pytest.fixture(scope="module")
 def lib():

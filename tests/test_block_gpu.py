@@ -226,3 +226,25 @@ def test_block_graph_replays_equal_eager():
         torch.cuda.synchronize()
         assert torch.equal(static_out, ref), f"replay {replay}"
         _ = (torch.randn(1 << 16, device=DEV) * 2).sum().item()  # unrelated eager work between replays
+
+
+def test_blocks_chain_equals_block_by_block():
+    """same_l.blocks with attention="hip" (each block's last residual pass also making the next block's pre_norm DyT)
+    gives the block-by-block loop's values bit for bit, over four blocks (SiLU and sine gates), and matches the
+    "xla" chain at the contract on the output divided by its largest magnitude."""
+    announce("same-l blocks chain")
+    cfg_hip = SameConfig(channels=64, c_mults=(2,), stride=16, transformer_depth=4, sinusoidal_blocks=2,
+                         attention="hip")
+    cfg_xla = SameConfig(channels=64, c_mults=(2,), stride=16, transformer_depth=4, sinusoidal_blocks=2,
+                         attention="xla")
+    ps = [to_torch(block_params(128, 2, 384, seed=70 + i), DEV, torch.bfloat16) for i in range(4)]
+    x = dev(RNG.standard_normal((1, 600, 128)), torch.bfloat16)
+    chained = same_l.blocks(x, ps, cfg_hip)
+    h = x
+    for i, p in enumerate(ps):
+        h = same_l.block(h, p, i, cfg_hip)
+    assert torch.equal(chained, h)
+    ref = same_l.blocks(x, ps, cfg_xla).float().cpu().numpy()
+    got = chained.float().cpu().numpy()
+    scale = max(1.0, float(np.abs(ref).max()))
+    assert_bf16_parity(got / scale, ref / scale, f"4 blocks hip vs xla (/{scale:.3g})")
