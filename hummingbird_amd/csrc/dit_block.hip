@@ -59,6 +59,12 @@ struct Vec<float> {  // fp32
   __device__ static float round(float x) { return x; }
 };
 
+// The logistic function with the hardware exponential and reciprocal (v_exp_f32, v_rcp_f32): within a few fp32
+// units of the exactly rounded value, which the compute dtype's rounding that follows hides but for values on a
+// tie; in fp32 a relative error of about 1e-6 at |u| = 10. The library expf and the IEEE division took a fifth of
+// a gated residual pass (10.0 against 8.1 us for 1422 rows of 1536 bf16 values with the norm).
+__device__ __forceinline__ float sigmoid(float u) { return __builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * u)); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
@@ -136,7 +142,7 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(const T* __restrict
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         const float u = Vec<T>::round(1.f - g[j]);
-        xv[j] = Vec<T>::round(xv[j] * Vec<T>::round(1.f / (1.f + expf(-u))));
+        xv[j] = Vec<T>::round(xv[j] * Vec<T>::round(sigmoid(u)));
       }
     }
 #pragma unroll
@@ -193,7 +199,7 @@ __global__ __launch_bounds__(256) void residual_rms_kernel(
 #pragma unroll
         for (int j = 0; j < V; ++j) {
           const float u = Vec<T>::round(1.f - g[k][j]);
-          xv[k][j] = Vec<T>::round(xv[k][j] * Vec<T>::round(1.f / (1.f + expf(-u))));
+          xv[k][j] = Vec<T>::round(xv[k][j] * Vec<T>::round(sigmoid(u)));
         }
       }
 #pragma unroll
