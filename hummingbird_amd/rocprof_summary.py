@@ -103,30 +103,41 @@ def agent(pmc_dir: Path) -> dict[str, int]:
 
 
 def counter_section(dirs: list[Path]) -> list[str]:
-    """Markdown table of the hardware counters of one or more `--pmc` passes, with the derived fractions:
-    matrix-core busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE / XCDs) (GRBM_GUI_ACTIVE is summed
-    over the XCDs, the busy cycles over the SIMDs), and LDS bank-conflict cycles per LDS-active cycle."""
+    """Markdown table of the hardware counters of one or more `--pmc` passes, with the derived fractions whose inputs
+    were collected: matrix-core busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE / XCDs) (GRBM_GUI_ACTIVE is
+    summed over the XCDs, the busy cycles over the SIMDs); LDS bank-conflict cycles per LDS-active cycle; and, per
+    wave-cycle (SQ_WAVE_CYCLES), the cycles a wave has a VALU instruction in flight (SQ_ACTIVE_INST_VALU), waits on a
+    dependency or counter (SQ_WAIT_ANY) and waits for its next instruction to issue (SQ_WAIT_INST_ANY); and the share
+    of matrix-core busy cycles with VALU work executing beside them (SQ_VALU_MFMA_COEXEC_CYCLES)."""
     merged: dict[str, dict[str, float]] = collections.defaultdict(dict)
     info = agent(dirs[0])
     for d in dirs:
         for k, cs in all_counters(d).items():
             merged[k].update(cs)
     names = sorted({c for cs in merged.values() for c in cs})
+
+    def busy(cs):
+        if "SQ_VALU_MFMA_BUSY_CYCLES" not in cs or not cs.get("GRBM_GUI_ACTIVE"):
+            return None
+        return cs["SQ_VALU_MFMA_BUSY_CYCLES"] / (info["Simd_Count"] * cs["GRBM_GUI_ACTIVE"] / info["Num_Xcc"])
+
+    def ratio(num, den):
+        return lambda cs: cs[num] / cs[den] if num in cs and cs.get(den) else None
+    derived = [("MFMA busy", busy), ("LDS bank conflict / LDS active", ratio("SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE")),
+               ("VALU active / wave cycles", ratio("SQ_ACTIVE_INST_VALU", "SQ_WAVE_CYCLES")),
+               ("waiting / wave cycles", ratio("SQ_WAIT_ANY", "SQ_WAVE_CYCLES")),
+               ("waiting to issue / wave cycles", ratio("SQ_WAIT_INST_ANY", "SQ_WAVE_CYCLES")),
+               ("VALU beside MFMA / MFMA busy", ratio("SQ_VALU_MFMA_COEXEC_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES"))]
+    derived = [(n, f) for n, f in derived if any(f(cs) is not None for cs in merged.values())]
     lines = ["", "## Hardware counters (`--pmc`; average per dispatch, summed over the GPU)", "",
              f"GPU: {info['Cu_Count']} CUs, {info['Simd_Count']} SIMDs, {info['Num_Xcc']} XCDs.", "",
-             "| kernel | " + " | ".join(names) + " | MFMA busy | LDS bank conflict / LDS active |",
-             "|---|" + "---|" * (len(names) + 2)]
+             "| kernel | " + " | ".join(names + [n for n, _ in derived]) + " |",
+             "|---|" + "---|" * (len(names) + len(derived))]
     for k in sorted(merged):
         cs = merged[k]
-        busy = "-"
-        if "SQ_VALU_MFMA_BUSY_CYCLES" in cs and cs.get("GRBM_GUI_ACTIVE"):
-            cycles = cs["GRBM_GUI_ACTIVE"] / info["Num_Xcc"]
-            busy = f"{cs['SQ_VALU_MFMA_BUSY_CYCLES'] / (info['Simd_Count'] * cycles):.1%}"
-        conf = "-"
-        if cs.get("SQ_LDS_IDX_ACTIVE") and "SQ_LDS_BANK_CONFLICT" in cs:
-            conf = f"{cs['SQ_LDS_BANK_CONFLICT'] / cs['SQ_LDS_IDX_ACTIVE']:.1%}"
-        lines.append(f"| `{k}` | " + " | ".join(f"{cs[c]:.4g}" if c in cs else "-" for c in names)
-                     + f" | {busy} | {conf} |")
+        vals = [f"{cs[c]:.4g}" if c in cs else "-" for c in names]
+        vals += [f"{v:.1%}" if (v := f(cs)) is not None else "-" for _, f in derived]
+        lines.append(f"| `{k}` | " + " | ".join(vals) + " |")
     return lines
 
 
