@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from hummingbird_amd import dit, elementwise, same_l, workloads, xla_chain
-from hummingbird_amd.config import MEDIUM_DIT, MEDIUM_SAME_L
+from hummingbird_amd.config import MEDIUM_DIT, MEDIUM_SAME_L, SameConfig
 from hummingbird_amd.dtypes import FP16
 from oracle import band as oband
 from oracle import block as oblock
@@ -200,3 +200,21 @@ def test_same_l_attention_fp16_preset_hip_vs_xla():
     assert got.dtype == H16
     ref = same_l.attention(x, block, dataclasses.replace(cfg, attention="xla"), lam=lam, dtype=FP16)
     assert_bf16_parity(got.float().cpu().numpy(), ref.float().cpu().numpy(), "same_l fp16")
+
+
+def test_same_l_blocks_fp16_hip_vs_xla():
+    """Two SAME-L decoder blocks (a SiLU and a sine block; dim 128 = 2 heads of 64, ff 384, half-width 17) in half
+    through `same_l.blocks`: attention="hip" (band kernel, hb_dyt, hb_glu, hb_residual_dyt) against "xla", at the
+    contract on the output divided by its largest magnitude."""
+    announce("same_l.blocks FP16")
+    from tests.block_util import block_params, to_torch
+    kw = dict(channels=64, c_mults=(2,), stride=16, transformer_depth=2, sinusoidal_blocks=2)  # block 1 has the sine
+    ps = [to_torch(block_params(128, 2, 384, seed=90 + i), DEV, H16) for i in (2, 3)]
+    x = torch.from_numpy(np.random.default_rng(91).standard_normal((1, 700, 128)).astype(np.float32)).to(DEV, H16)
+    cfg = SameConfig(**kw, attention="hip")
+    assert not cfg.sinusoidal(0) and cfg.sinusoidal(1)
+    got = same_l.blocks(x, ps, cfg)
+    ref = same_l.blocks(x, ps, dataclasses.replace(cfg, attention="xla"))
+    assert got.dtype == H16 and ref.dtype == H16
+    scale = max(1.0, float(ref.float().abs().max()))
+    assert_bf16_parity(got.float().cpu().numpy() / scale, ref.float().cpu().numpy() / scale, "blocks fp16 (/max)")
