@@ -59,6 +59,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--sampler-only", action="store_true",
                     help="instead of the clip benchmark: the whole 120 s render of the medium DiT (8 pingpong steps "
                          "x 24 blocks, eager and as one HIP graph), one JSON line; for profiling under rocprofv3")
+    ap.add_argument("--decoder-only", action="store_true",
+                    help="instead of the clip benchmark: the SAME-L decoder's 12 blocks for a 120 s clip at the "
+                         "reference's decoder geometry, chained and block by block, one JSON line; for profiling")
     ap.add_argument("--no-tune", action="store_true",
                     help="skip the sampler timing with TunableOp-selected GEMMs (whose search launches thousands of "
                          "candidate kernels; for profiling the loop itself)")
@@ -647,6 +650,10 @@ def main() -> int:
         return 0
     if args.sampler_only:
         print(json.dumps({"sampler_120s": sampler_shape(dev, tune=not args.no_tune)}), flush=True)
+        return 0
+    if args.decoder_only:
+        gen = torch.Generator(device=dev).manual_seed(0)
+        print(json.dumps({"same_l_decoder_120s": decoder_shape(dev, gen)}), flush=True)
         return 0
 
     # ---- dense inputs (two qkv buffers alternate, as consecutive blocks would) ----
