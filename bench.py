@@ -409,8 +409,8 @@ def decoder_shape(dev, gen) -> dict:
     """The SAME-L decoder's 12 blocks for a 120 s clip at the reference's medium geometry (1358 latents x 17 = 23086
     frames, dim 1536 = 24 heads of 64, ff 4608, half-width 17, the last 8 blocks with the sine gate; random weights,
     bf16): ms per clip for the chained loop (`same_l.blocks`, each block handing the next its pre_norm DyT) and for
-    the block-by-block loop, medians of 3 after one warm-up. The reference's published figure for its whole decode
-    (these blocks plus the bottleneck, token interleave and output mapping) is 61 ms on a TPU v6e-1."""
+    the block-by-block loop, medians of 7 interleaved runs after one warm-up each. The reference's published figure for its whole decode (these blocks plus the
+    bottleneck, token interleave and output mapping) is 61 ms on a TPU v6e-1."""
     import torch
 
     from hummingbird_amd import same_l
@@ -448,21 +448,23 @@ def decoder_shape(dev, gen) -> dict:
             h = same_l.block(h, p, i, cfg)
         return h
 
-    def ms(fn, n=3) -> float:
+    def once(fn) -> float:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
         fn()
+        b.record()
         torch.cuda.synchronize()
-        ts = []
-        for _ in range(n):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            fn()
-            b.record()
-            torch.cuda.synchronize()
-            ts.append(a.elapsed_time(b))
-        return round(float(np.median(ts)), 3)
+        return a.elapsed_time(b)
+    chained(), one_by_one()
+    torch.cuda.synchronize()
+    times = {"chained": [], "one_by_one": []}
+    for _ in range(7):  # the two loops interleaved, so that a drift of the clock touches both alike
+        times["chained"].append(once(chained))
+        times["one_by_one"].append(once(one_by_one))
     res = {"shape": {"S": S, "dim": dim, "heads": cfg.num_heads, "ff": ff, "w": cfg.sub_chunk_size,
                      "blocks": cfg.transformer_depth, "sine_blocks": cfg.sinusoidal_blocks},
-           "chained_ms_per_clip": ms(chained), "block_by_block_ms_per_clip": ms(one_by_one),
+           "chained_ms_per_clip": round(float(np.median(times["chained"])), 3),
+           "block_by_block_ms_per_clip": round(float(np.median(times["one_by_one"])), 3),
            "reference_whole_decode_ms_tpu_v6e": 61.0}
     del params
     return res

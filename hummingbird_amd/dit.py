@@ -267,7 +267,8 @@ def _block_fused(h: torch.Tensor, block: dict, static: dict, adaln: tuple, index
 
 
 def _fp32_norms(block: dict) -> dict:
-    """A view of a block's parameters with its norm scales in fp32 (the other tensors shared)."""
+    """A view of a block's parameters with its norm scales and glu_proj's bias in fp32, the forms the HIP kernels take
+    (the other tensors shared), so that no call converts them again."""
     out = dict(block)
     for key in ("pre_norm", "cross_attend_norm", "ff_norm"):
         out[key] = {"weight": block[key]["weight"].float().contiguous()}
@@ -275,6 +276,9 @@ def _fp32_norms(block: dict) -> dict:
         out[attn] = dict(block[attn])
         for norm in ("q_norm", "k_norm"):
             out[attn][norm] = {"weight": block[attn][norm]["weight"].float().contiguous()}
+    glu = block["ff"]["glu_proj"]
+    if glu.get("bias") is not None:  # hb_glu reads it in fp32; the torch route casts it to the compute dtype again
+        out["ff"] = {**block["ff"], "glu_proj": {**glu, "bias": glu["bias"].float().contiguous()}}
     return out
 
 
