@@ -628,7 +628,7 @@ def ceiling_rows(lib, sp, stream, dev, rounds: int = 3) -> list[dict]:
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1 (the kernels shard by "
+        print(json.dumps({"error": "bench.py measures one GPU only; run with --gpus 1 (the kernels shard by "
                                    "(batch, head) and by sequence with a halo, which is described but not built)"}))
         return 2
 

@@ -18,7 +18,8 @@ This package restates, in NumPy, the arithmetic of the reference's XLA attention
 * `oracle.bf16` -- round-to-nearest-even bfloat16 emulation for the cast points.
 
 Only `tests/`, `__graft_entry__.smoke()` and `bench.py`'s CPU-baseline leg may import this package,
-and only as the checker or the timed CPU baseline. The product (`hummingbird_amd`) never imports it.
+and only as the reference results that outputs are compared against or as the timed CPU baseline. The product
+(`hummingbird_amd`) never imports it.
 
 How each function is pinned (the checks live in tests/test_oracle.py):
 
