@@ -64,6 +64,39 @@ int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int 
   return HB_OK;
 }
 
+namespace {
+int64_t floor_div(int64_t a, int64_t b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }  // b > 0
+}  // namespace
+
+bool regions_overlap(const void* a, int64_t as, int64_t ca, const void* b, int64_t bs, int64_t cb, int64_t N,
+                     int esize) {
+  if (!a || !b || N < 1 || ca < 1 || cb < 1) return false;
+  const int64_t pa = static_cast<int64_t>(reinterpret_cast<uintptr_t>(a));
+  const int64_t pb = static_cast<int64_t>(reinterpret_cast<uintptr_t>(b));
+  const int64_t wa = ca * esize, wb = cb * esize;  // bytes of one row of each
+  if (as == bs) {
+    // Row i of a, [pa + i S, pa + i S + wa), meets row j of b iff -wa < d + k S < wb with d = pa - pb and
+    // k = i - j in [-(N - 1), N - 1]: an interval of k, checked exactly.
+    const int64_t S = as * esize, d = pa - pb;
+    int64_t lo = floor_div(-wa - d, S) + 1, hi = -floor_div(d - wb, S) - 1;
+    if (lo < -(N - 1)) lo = -(N - 1);
+    if (hi > N - 1) hi = N - 1;
+    return lo <= hi;
+  }
+  const int64_t ea = pa + (N - 1) * as * esize + wa, eb = pb + (N - 1) * bs * esize + wb;
+  return pa < eb && pb < ea;
+}
+
+int check_no_overlap(const char* what, const char* out_name, const void* out, int64_t out_stride, int64_t out_cols,
+                     const char* in_name, const void* in, int64_t in_stride, int64_t in_cols, int64_t N, int esize,
+                     bool in_place_ok) {
+  if (in_place_ok && out == in && out_stride == in_stride && out_cols == in_cols) return HB_OK;
+  if (regions_overlap(out, out_stride, out_cols, in, in_stride, in_cols, N, esize))
+    return fail(HB_ERR_STRIDE, "%s: %s overlaps %s%s", what, out_name, in_name,
+                in_place_ok ? " (only the same buffer with the same row stride may be updated in place)" : "");
+  return HB_OK;
+}
+
 }  // namespace hb
 
 extern "C" {

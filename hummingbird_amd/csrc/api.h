@@ -32,6 +32,20 @@ struct DenseLayout {
 DenseLayout dense_layout(int dtype, int B, int L, int H, int D);
 
 int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int half);
+
+// Whether two row-strided regions share a byte: N rows of ca (cb) elements of `esize` bytes, starting at a (b),
+// rows `as` (`bs`) elements apart (strides >= the row widths). With equal strides the test is exact, so column
+// slices of one wider buffer that interleave without sharing elements do not overlap; with different strides it is
+// the conservative test of the two byte extents. NULL never overlaps.
+bool regions_overlap(const void* a, int64_t as, int64_t ca, const void* b, int64_t bs, int64_t cb, int64_t N,
+                     int esize);
+// The aliasing rule of the row-wise entry points for an output `out` (N x out_cols) against an input `in`
+// (N x in_cols): when `in_place_ok` the output may be the input itself (same pointer, row stride and width: every
+// element is read before it is written, by the thread that writes it); otherwise, and for any other placement, the
+// two must share no element.
+int check_no_overlap(const char* what, const char* out_name, const void* out, int64_t out_stride, int64_t out_cols,
+                     const char* in_name, const void* in, int64_t in_stride, int64_t in_cols, int64_t N, int esize,
+                     bool in_place_ok);
 // Multiprocessor (CU) count of the current device, queried once per device (256 if the query fails).
 int device_cus();
 

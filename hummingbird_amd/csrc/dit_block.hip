@@ -327,6 +327,9 @@ int hb_rms_modulate(hipStream_t stream, const void* x, int dtype, int64_t x_row_
     if ((st = check_tensor("rms_modulate", "scale", scale, stride, C, dtype, true))) return st;
     if ((st = check_tensor("rms_modulate", "shift", shift, stride, C, dtype, true))) return st;
   }
+  if ((st = check_no_overlap("rms_modulate", "out", out, out_row_stride, C, "x", x, x_row_stride, C, N,
+                             dtype == HB_F32 ? 4 : 2, false)))
+    return st;
   if (dtype == HB_BF16)
     launch_rms<uint16_t>(stream, x, x_row_stride, weight, eps, scale, shift, mod_batch_stride, rows_per_batch, out,
                          out_row_stride, N, C);
@@ -357,6 +360,14 @@ int hb_gated_residual(hipStream_t stream, const void* h, int dtype, int64_t h_ro
     if ((st = check_tensor("gated_residual", "gate", gate, several ? gate_batch_stride : C, C, dtype, true))) return st;
   }
   if (memory < 0) return fail(HB_ERR_SHAPE, "gated_residual: memory must be >= 0");
+  {
+    const int es = dtype == HB_F32 ? 4 : 2;
+    if ((st = check_no_overlap("gated_residual", "out", out, out_row_stride, C, "h", h, h_row_stride, C, N, es,
+                               false)) ||
+        (st = check_no_overlap("gated_residual", "out", out, out_row_stride, C, "x", x, x_row_stride, C, N, es,
+                               false)))
+      return st;
+  }
   if (dtype == HB_BF16)
     launch_residual<uint16_t>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local,
                               memory, rows_per_batch, out, out_row_stride, N, C);
@@ -397,6 +408,16 @@ int hb_residual_rms(hipStream_t stream, const void* h, int dtype, int64_t h_row_
       return st;
     if (scale && ((st = check_tensor("residual_rms", "scale", scale, several ? mod_batch_stride : C, C, dtype, true)) ||
                   (st = check_tensor("residual_rms", "shift", shift, several ? mod_batch_stride : C, C, dtype, true))))
+      return st;
+  }
+  {
+    const int es = dtype == HB_F32 ? 4 : 2;
+    const char* w = "residual_rms";
+    if ((st = check_no_overlap(w, "out_h", out_h, out_row_stride, C, "h", h, h_row_stride, C, N, es, false)) ||
+        (st = check_no_overlap(w, "out_h", out_h, out_row_stride, C, "x", x, x_row_stride, C, N, es, false)) ||
+        (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "h", h, h_row_stride, C, N, es, false)) ||
+        (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "x", x, x_row_stride, C, N, es, false)) ||
+        (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "out_h", out_h, out_row_stride, C, N, es, false)))
       return st;
   }
   if (dtype == HB_BF16)

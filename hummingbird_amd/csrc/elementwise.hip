@@ -213,6 +213,8 @@ int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, c
   int st = check_rows("dyt", dtype, x, x_row_stride, out, out_row_stride, N, C, C);
   if (st) return st;
   if (!dyt) return fail(HB_ERR_NULL, "dyt parameters must be non-NULL");
+  const int es = dtype == HB_F32 ? 4 : 2;
+  if ((st = check_no_overlap("dyt", "out", out, out_row_stride, C, "x", x, x_row_stride, C, N, es, false))) return st;
   const int chunks = C / (dtype == HB_F32 ? 4 : 8);
   if (dtype == HB_BF16)
     hipLaunchKernelGGL(ew::dyt_kernel<uint16_t>, row_grid(N, chunks), dim3(256), 0, stream,
@@ -233,6 +235,10 @@ int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_str
   clear_error();
   int st = check_rows("glu", dtype, proj, proj_row_stride, out, out_row_stride, N, F, static_cast<int64_t>(2) * F);
   if (st) return st;
+  // A thread reads the value and gate chunks of its output chunk, which other threads' outputs could cover.
+  if ((st = check_no_overlap("glu", "out", out, out_row_stride, F, "proj", proj, proj_row_stride,
+                             static_cast<int64_t>(2) * F, N, dtype == HB_F32 ? 4 : 2, false)))
+    return st;
   const int chunks = F / (dtype == HB_F32 ? 4 : 8);
   const dim3 grid = row_grid(N, chunks);
   if (dtype == HB_F16) {
@@ -277,10 +283,14 @@ int hb_residual_dyt(hipStream_t stream, const void* h, int dtype, int64_t h_row_
   if (!dyt != !out_y) return fail(HB_ERR_NULL, "residual_dyt: dyt and out_y are given together or not at all");
   if (out_y && reinterpret_cast<uintptr_t>(out_y) % 16)
     return fail(HB_ERR_STRIDE, "residual_dyt: out_y must be 16-byte aligned");
-  if (out_y && (out_y == h || out_y == x || out_y == out_h))
-    return fail(HB_ERR_STRIDE, "residual_dyt: out_y must not alias h, x or out_h");
-  if (out_h == x || (out_h == h && h_row_stride != out_row_stride))
-    return fail(HB_ERR_STRIDE, "residual_dyt: out_h may alias h (with the same row stride) but not x");
+  const int es = dtype == HB_F32 ? 4 : 2;
+  const char* w = "residual_dyt";
+  if ((st = check_no_overlap(w, "out_h", out_h, out_row_stride, C, "h", h, h_row_stride, C, N, es, true)) ||
+      (st = check_no_overlap(w, "out_h", out_h, out_row_stride, C, "x", x, x_row_stride, C, N, es, false)) ||
+      (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "h", h, h_row_stride, C, N, es, false)) ||
+      (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "x", x, x_row_stride, C, N, es, false)) ||
+      (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "out_h", out_h, out_row_stride, C, N, es, false)))
+    return st;
   const dim3 grid = row_grid(N, C / (dtype == HB_F32 ? 4 : 8));
   if (dtype == HB_BF16)
     hipLaunchKernelGGL(ew::residual_dyt_kernel<uint16_t>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(h),

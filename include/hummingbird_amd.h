@@ -218,7 +218,8 @@ int hb_cross_attend(hipStream_t stream, const void* q, int dtype, int64_t row_st
  *            holds it.
  *   x, proj, out : N rows with row strides in elements (multiples of 8 for bf16 and half, 4 for fp32), 16-byte
  *                  aligned; C and F multiples of 8 (bf16, half) or 4 (fp32);  dtype: HB_BF16, HB_F16 or HB_F32 (input
- *                  and output). */
+ *                  and output). out shares no element with the input (HB_ERR_STRIDE otherwise; column slices of one
+ *                  wider buffer that interleave without sharing elements are fine). */
 int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const float* dyt, void* out,
            int64_t out_row_stride, int64_t N, int C);
 int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_stride, const float* bias,
@@ -228,9 +229,9 @@ int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_str
  *                     the projection's bias add (same_l._linear), each sum rounded to the compute dtype; `bias` (C
  *                     floats holding values of the compute dtype) may be NULL. With `dyt` (packed as for hb_dyt) also
  *                     out_y = cast(DyT(out_h)), the input of the next GEMM (ff_norm, or the next block's pre_norm);
- *                     `dyt` and `out_y` are both given or both NULL. out_h may be h itself (same row stride); out_y
- *                     aliases nothing. out_h and out_y share `out_row_stride`. One pass where the XLA chain makes two or
- *                     three. */
+ *                     `dyt` and `out_y` are both given or both NULL. out_h may be h itself (same row stride) and
+ *                     otherwise shares no element with h or x; out_y shares none with h, x or out_h. out_h and out_y
+ *                     share `out_row_stride`. One pass where the XLA chain makes two or three. */
 int hb_residual_dyt(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* x,
                     int64_t x_row_stride, const float* bias, const float* dyt, void* out_h, void* out_y,
                     int64_t out_row_stride, int64_t N, int C);
@@ -250,7 +251,9 @@ int hb_residual_dyt(hipStream_t stream, const void* h, int dtype, int64_t h_row_
  *                       gate: one row of C values per batch, `gate_batch_stride` elements apart; x_bias, local: C
  *                       values.
  *   All tensors are of `dtype` (HB_BF16, HB_F16 or HB_F32) except `weight`; row strides in elements, multiples of
- *   8 (bf16, half) or 4 (fp32); every pointer 16-byte aligned; C a multiple of 8 (bf16, half) or 4 (fp32). */
+ *   8 (bf16, half) or 4 (fp32); every pointer 16-byte aligned; C a multiple of 8 (bf16, half) or 4 (fp32). The
+ *   row outputs (out; out_h and out_y) share no element with the row inputs (x; h and x) or with each other
+ *   (HB_ERR_STRIDE otherwise). */
 int hb_rms_modulate(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const float* weight,
                     float eps, const void* scale, const void* shift, int64_t mod_batch_stride, int rows_per_batch,
                     void* out, int64_t out_row_stride, int64_t N, int C);

@@ -202,6 +202,36 @@ def test_dit_block_entry_points_reject_before_any_launch(lib):
     assert res(gate=fake, gs=32) == 7 and res(local=fake + 2) == 7 and res(memory=-1) == 2
 
 
+def test_row_outputs_that_overlap_their_inputs_are_refused(lib):
+    """Every row-wise entry point refuses an output that shares an element with a row input or with the other
+    output, before any launch (HB_ERR_STRIDE; fake, never dereferenced addresses): partial overlaps within a row and
+    across rows, and in place where the kernel's operands are restrict-qualified. Only hb_residual_dyt may update h
+    in place (its test on the GPU); interleaved column slices of one buffer are accepted (GPU test)."""
+    a, b, c = 0x100000, 0x200000, 0x300000
+    N, C = 20, 64                                    # bf16 rows of 128 bytes at a row stride of 64 elements
+    dyt = lambda x, out: lib.hb_dyt(None, x, 0, C, c + 0x80000, out, C, N, C)  # noqa: E731
+    assert dyt(a, a) == 7 and dyt(a, a + 16) == 7 and dyt(a, a + 128 * (N - 1)) == 7 and dyt(a + 16, a) == 7
+    F = 64                                           # glu: proj rows hold 2F, out rows F
+    glu = lambda proj, ps, out, os_: lib.hb_glu(None, proj, 0, ps, None, 0, out, os_, N, F)  # noqa: E731
+    assert glu(a, 2 * F, a + 2 * F, 2 * F) == 7      # out over the gate half of proj's rows
+    assert glu(a, 2 * F, a + 2 * 2 * F * (N - 1), F) == 7  # out starts on proj's last row
+    rd = lambda h, x, oh, oy, os_=C: lib.hb_residual_dyt(None, h, 0, C, x, C, None, c + 0x80000 if oy else None,  # noqa: E731
+                                                         oh, oy, os_, N, C)
+    assert rd(a, b, a + 16, None) == 7               # out_h part of h, not h itself
+    assert rd(a, b, b + 128 * 3, None) == 7          # out_h over rows of x
+    assert rd(a, b, a, a + 128 * (N - 1)) == 7       # out_y over h's (and out_h's) last row
+    assert rd(a, b, c, c + 64) == 7                  # out_y inside out_h's first row
+    assert rd(a, b, c, b + 32) == 7                  # out_y over x
+    rms = lambda x, out: lib.hb_rms_modulate(None, x, 0, C, c + 0x80000, 1e-5, None, None, C, N, out, C, N, C)  # noqa: E731
+    assert rms(a, a) == 7 and rms(a, a + 128 * 5 + 48) == 7
+    res = lambda h, x, out: lib.hb_gated_residual(None, h, 0, C, x, C, None, None, C, None, 0, N, out, C, N, C)  # noqa: E731
+    assert res(a, b, a) == 7 and res(a, b, b + 16) == 7
+    rr = lambda oh, oy: lib.hb_residual_rms(None, a, 0, C, b, C, None, None, C, None, 0, c + 0x80000, 1e-5,  # noqa: E731
+                                            None, None, C, N, oh, oy, C, N, C)
+    assert rr(a, c) == 7 and rr(c, c) == 7 and rr(c, b + 128 * 2) == 7 and rr(c, c + 128 * (N - 1)) == 7
+    assert "overlaps" in lib.hb_last_error().decode()
+
+
 def test_residual_rms_rejects_before_any_launch(lib):
     fake = 0x100000
     call = lambda **kw: lib.hb_residual_rms(  # noqa: E731

@@ -199,6 +199,45 @@ def test_residual_dyt_in_place():
     assert torch.equal(h, ref_h) and torch.equal(y, ref_y)
 
 
+def test_row_ops_on_interleaved_column_slices():
+    """Inputs and outputs as interleaved column slices of one wide buffer (same row stride, no element shared) pass
+    the C ABI's overlap check, and hb_residual_dyt, hb_dyt, hb_rms_modulate and hb_residual_rms write exactly what
+    they write into separate tensors, leaving the other columns untouched."""
+    announce("row ops on interleaved column slices")
+    from hummingbird_amd import _lib
+    lib, stream = _lib.load(), torch.cuda.current_stream().cuda_stream
+    n, c = 300, 256
+    buf = dev(RNG.standard_normal((n, 6 * c)), torch.bfloat16)
+    keep = buf.clone()
+    h, x, oh, oy, od, orm = (buf[:, i * c:(i + 1) * c] for i in range(6))
+    norm = {"alpha": torch.tensor(0.6, device=DEV), "gamma": dev(1 + 0.1 * RNG.standard_normal(c)),
+            "beta": dev(0.1 * RNG.standard_normal(c))}
+    ref_h, ref_y = elementwise.residual_dyt(h.contiguous(), x.contiguous(), norm=norm)
+    ref_d = elementwise.dyt(h.contiguous(), norm)
+    w = dev(1 + 0.1 * RNG.standard_normal(c))
+    ref_r = elementwise.rms_modulate(x.contiguous().unsqueeze(0), w, 1e-6)[0]
+    params = elementwise.pack_dyt(norm, c, h.device)
+    rs = 6 * c
+    _lib.check(lib.hb_residual_dyt(stream, h.data_ptr(), _lib.HB_BF16, rs, x.data_ptr(), rs, 0, params.data_ptr(),
+                                   oh.data_ptr(), oy.data_ptr(), rs, n, c), "residual_dyt")
+    _lib.check(lib.hb_dyt(stream, h.data_ptr(), _lib.HB_BF16, rs, params.data_ptr(), od.data_ptr(), rs, n, c), "dyt")
+    _lib.check(lib.hb_rms_modulate(stream, x.data_ptr(), _lib.HB_BF16, rs, w.data_ptr(), 1e-6, None, None, c, n,
+                                   orm.data_ptr(), rs, n, c), "rms_modulate")
+    torch.cuda.synchronize()
+    assert torch.equal(oh, ref_h) and torch.equal(oy, ref_y) and torch.equal(od, ref_d) and torch.equal(orm, ref_r)
+    assert torch.equal(buf[:, :2 * c], keep[:, :2 * c])  # the inputs
+    # hb_residual_rms: h and x in columns 0 and 1, the two outputs in columns 2 and 3 of a fresh copy
+    buf2 = keep.clone()
+    h2, x2, oh2, oy2 = (buf2[:, i * c:(i + 1) * c] for i in range(4))
+    ref_h2, ref_y2 = elementwise.residual_rms(h2.contiguous().unsqueeze(0), x2.contiguous().unsqueeze(0), w, 1e-6)
+    _lib.check(lib.hb_residual_rms(stream, h2.data_ptr(), _lib.HB_BF16, rs, x2.data_ptr(), rs, None, None, c, None,
+                                   0, w.data_ptr(), 1e-6, None, None, c, n, oh2.data_ptr(), oy2.data_ptr(), rs, n, c),
+               "residual_rms")
+    torch.cuda.synchronize()
+    assert torch.equal(oh2, ref_h2[0]) and torch.equal(oy2, ref_y2[0])
+    assert torch.equal(buf2[:, :2 * c], keep[:, :2 * c]) and torch.equal(buf2[:, 4 * c:], keep[:, 4 * c:])
+
+
 def test_block_graph_replays_equal_eager():
     """The whole SAME-L block with attention="hip" (hb_dyt, the band kernel, hb_glu, hb_residual_dyt and the torch
     GEMMs) captured as one HIP graph: three replays with new inputs, eager work in between, each bit-identical to
