@@ -97,6 +97,15 @@ int check_no_overlap(const char* what, const char* out_name, const void* out, in
   return HB_OK;
 }
 
+int check_disjoint(const char* what, const char* a_name, const void* a, int64_t a_bytes, const char* b_name,
+                   const void* b, int64_t b_bytes) {
+  if (!a || !b || a_bytes <= 0 || b_bytes <= 0) return HB_OK;
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  if (pa < pb + static_cast<uintptr_t>(b_bytes) && pb < pa + static_cast<uintptr_t>(a_bytes))
+    return fail(HB_ERR_STRIDE, "%s: %s overlaps %s", what, a_name, b_name);
+  return HB_OK;
+}
+
 }  // namespace hb
 
 extern "C" {

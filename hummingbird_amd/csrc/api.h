@@ -39,6 +39,12 @@ int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int 
 // the conservative test of the two byte extents. NULL never overlaps.
 bool regions_overlap(const void* a, int64_t as, int64_t ca, const void* b, int64_t bs, int64_t cb, int64_t N,
                      int esize);
+// Bytes spanned by N rows of C elements of `esize` bytes, rows `stride` elements apart.
+inline int64_t rows_bytes(int64_t N, int64_t stride, int64_t C, int esize) { return ((N - 1) * stride + C) * esize; }
+// Fails with HB_ERR_STRIDE if the byte ranges [a, a + a_bytes) and [b, b + b_bytes) intersect (NULL never does):
+// an output or workspace of the attention and projection entry points against the buffers the same call reads.
+int check_disjoint(const char* what, const char* a_name, const void* a, int64_t a_bytes, const char* b_name,
+                   const void* b, int64_t b_bytes);
 // The aliasing rule of the row-wise entry points for an output `out` (N x out_cols) against an input `in`
 // (N x in_cols): when `in_place_ok` the output may be the input itself (same pointer, row stride and width: every
 // element is read before it is written, by the thread that writes it); otherwise, and for any other placement, the

@@ -39,24 +39,43 @@ extern "C" int hb_band_diffattn(hipStream_t stream, const void* qkv, int dtype, 
   if (reinterpret_cast<uintptr_t>(qkv) % 16) return fail(HB_ERR_STRIDE, "qkv must be 16-byte aligned");
   if (half > 0 && (reinterpret_cast<uintptr_t>(cos) % 16 || reinterpret_cast<uintptr_t>(sin) % 16))
     return fail(HB_ERR_STRIDE, "cos and sin must be 16-byte aligned");
+  // Outputs against the buffers the call reads, checked after the workspace is known to be valid.
+  auto overlaps = [&]() {
+    const int es = dtype == HB_F32 ? 4 : 2;
+    const int64_t HD = static_cast<int64_t>(H) * D, rows = static_cast<int64_t>(B) * S, ob = rows * HD * es;
+    const int64_t qb = rows_bytes(rows, row_stride, 5 * HD, es);
+    // the bytes of the workspace this call writes (none when the ring kernel runs)
+    const int64_t wb = workspace ? static_cast<int64_t>(hb_band_workspace_size(dtype, B, S, H, D, half, window)) : 0;
+    int ov;
+    if ((ov = check_disjoint("band", "out", out, ob, "qkv", qkv, qb)) ||
+        (ov = check_disjoint("band", "workspace", workspace, wb, "qkv", qkv, qb)) ||
+        (ov = check_disjoint("band", "workspace", workspace, wb, "out", out, ob)))
+      return ov;
+    return static_cast<int>(HB_OK);
+  };
   if (dtype == HB_F32) {
     if (reinterpret_cast<uintptr_t>(out) % 16) return fail(HB_ERR_STRIDE, "fp32 out must be 16-byte aligned");
     if (workspace) {
       const size_t need = dense_layout(HB_F32, B, S, H, D).total_bytes;
       if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(HB_ERR_WORKSPACE, "workspace must be 256-byte aligned");
       if (workspace_bytes < need) return fail(HB_ERR_WORKSPACE, "workspace holds %zu bytes, needs %zu", workspace_bytes, need);
+      if ((st = overlaps())) return st;
       return launch_band_f32_ws(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D,
                                 workspace);
     }
+    if ((st = overlaps())) return st;
     return launch_band_f32(stream, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D);
   }
   if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
-  if (band_ring_supported(dtype, D, half, window))
+  if (band_ring_supported(dtype, D, half, window)) {
+    if ((st = overlaps())) return st;
     return launch_band_ring(stream, dtype, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H);
+  }
   const size_t need = band_tiled_layout(B, S, H, D).total_bytes;
   if (!workspace) return fail(HB_ERR_WORKSPACE, "this shape needs a workspace of %zu bytes (hb_band_workspace_size)", need);
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(HB_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (workspace_bytes < need) return fail(HB_ERR_WORKSPACE, "workspace holds %zu bytes, needs %zu", workspace_bytes, need);
+  if ((st = overlaps())) return st;
   return launch_band_tiled(stream, dtype, qkv, row_stride, q_dyt, k_dyt, cos, sin, half, window, lam, out, B, S, H, D,
                            workspace);
 }

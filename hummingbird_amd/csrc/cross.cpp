@@ -80,6 +80,10 @@ int hb_cross_prep(hipStream_t stream, const void* kv, int dtype, int64_t row_str
   const DenseLayout lay = dense_layout(dtype, B, Nk, H, D);
   st = check_workspace(workspace, workspace_bytes, lay.total_bytes);
   if (st) return st;
+  const int es = dtype == HB_F32 ? 4 : 2;
+  if ((st = check_disjoint("cross_prep", "workspace", workspace, static_cast<int64_t>(lay.total_bytes), "kv", kv,
+                           rows_bytes(static_cast<int64_t>(B) * Nk, row_stride, static_cast<int64_t>(3) * H * D, es))))
+    return st;
   if (dtype == HB_F32)
     return launch_dense_prep_f32(stream, kv, row_stride, kKSec, kKdSec, kVSec, k_weight, nullptr, nullptr, 0, nullptr,
                                  B, Nk, H, D, eps, lay, workspace);
@@ -100,6 +104,14 @@ int hb_cross_attend(hipStream_t stream, const void* q, int dtype, int64_t row_st
   const DenseLayout lay = dense_layout(dtype, B, Nk, H, D);
   st = check_workspace(workspace, workspace_bytes, lay.total_bytes);
   if (st) return st;
+  {
+    const int es = dtype == HB_F32 ? 4 : 2;
+    const int64_t HD = static_cast<int64_t>(H) * D, rows = static_cast<int64_t>(B) * L, ob = rows * HD * es;
+    if ((st = check_disjoint("cross_attend", "out", out, ob, "q", q, rows_bytes(rows, row_stride, 2 * HD, es))) ||
+        (st = check_disjoint("cross_attend", "out", out, ob, "workspace", workspace,
+                             static_cast<int64_t>(lay.total_bytes))))
+      return st;
+  }
   if (dtype == HB_F32) {
     if (reinterpret_cast<uintptr_t>(out) % 16) return fail(HB_ERR_STRIDE, "fp32 out must be 16-byte aligned");
     return launch_dense_attend_f32(stream, q, row_stride, kQdSec, q_weight, nullptr, nullptr, 0, eps, workspace, lam,

@@ -506,6 +506,18 @@ int launch_dense_attend_16bit(hipStream_t stream, int dtype, const void* q, int6
 // Sections of a to_qkv row [q | k | v | q_diff | k_diff] (dit.py:196-198), in units of H * D.
 constexpr int kSecK = 1, kSecV = 2, kSecQd = 3, kSecKd = 4;
 
+// The output of the attention stage: alignment, and no byte shared with qkv or the workspace it reads.
+static int out_checks(const void* qkv, int dtype, int64_t row_stride, const void* out, int B, int L, int H, int D,
+                      const void* workspace, const DenseLayout& lay) {
+  if (reinterpret_cast<uintptr_t>(out) % (dtype == HB_F32 ? 16 : 8))
+    return fail(HB_ERR_STRIDE, "out must be %d-byte aligned", dtype == HB_F32 ? 16 : 8);
+  const int es = dtype == HB_F32 ? 4 : 2;
+  const int64_t HD = static_cast<int64_t>(H) * D, rows = static_cast<int64_t>(B) * L, ob = rows * HD * es;
+  int st = check_disjoint("dense_attend", "out", out, ob, "qkv", qkv, rows_bytes(rows, row_stride, 5 * HD, es));
+  if (st) return st;
+  return check_disjoint("dense_attend", "out", out, ob, "workspace", workspace, static_cast<int64_t>(lay.total_bytes));
+}
+
 extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int64_t row_stride, const float* q_weight,
                              const float* k_weight, const float* cos, const float* sin, int half, const float* vmask,
                              int B, int L, int H, int D, float eps, void* workspace, size_t workspace_bytes) {
@@ -513,6 +525,11 @@ extern "C" int hb_dense_prep(hipStream_t stream, const void* qkv, int dtype, int
   const int st = dense_checks(qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, B, L, H, D, eps, workspace,
                               workspace_bytes, lay);
   if (st) return st;
+  const int es = dtype == HB_F32 ? 4 : 2;
+  if (const int ov = check_disjoint("dense_prep", "workspace", workspace, static_cast<int64_t>(lay.total_bytes), "qkv",
+                                    qkv, rows_bytes(static_cast<int64_t>(B) * L, row_stride,
+                                                    static_cast<int64_t>(5) * H * D, es)))
+    return ov;
   if (dtype == HB_F32)
     return launch_dense_prep_f32(stream, qkv, row_stride, kSecK, kSecKd, kSecV, k_weight, cos, sin, half, vmask, B, L,
                                  H, D, eps, lay, workspace);
@@ -529,15 +546,13 @@ extern "C" int hb_dense_attend(hipStream_t stream, const void* qkv, int dtype, i
     return fail(HB_ERR_NULL, "out must be non-NULL");
   }
   DenseLayout lay;
-  const int st = dense_checks(qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, B, L, H, D, eps, workspace,
-                              workspace_bytes, lay);
+  int st = dense_checks(qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, B, L, H, D, eps, workspace,
+                        workspace_bytes, lay);
   if (st) return st;
-  if (dtype == HB_F32) {
-    if (reinterpret_cast<uintptr_t>(out) % 16) return fail(HB_ERR_STRIDE, "fp32 out must be 16-byte aligned");
+  if ((st = out_checks(qkv, dtype, row_stride, out, B, L, H, D, workspace, lay))) return st;
+  if (dtype == HB_F32)
     return launch_dense_attend_f32(stream, qkv, row_stride, kSecQd, q_weight, cos, sin, half, eps, workspace, lam, out,
                                    B, L, L, H, D, lay);
-  }
-  if (reinterpret_cast<uintptr_t>(out) % 8) return fail(HB_ERR_STRIDE, "out must be 8-byte aligned");
   return launch_dense_attend_16bit(stream, dtype, qkv, row_stride, kSecQd, q_weight, k_weight, cos, sin, half, eps, lam,
                                    out, B, L, L, H, D, lay, workspace);
 }
@@ -549,6 +564,13 @@ extern "C" int hb_dense_diffattn(hipStream_t stream, const void* qkv, int dtype,
   if (!out) {
     clear_error();
     return fail(HB_ERR_NULL, "out must be non-NULL");
+  }
+  {  // everything the attention stage checks, before the prep stage launches
+    DenseLayout lay;
+    int st = dense_checks(qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, B, L, H, D, eps, workspace,
+                          workspace_bytes, lay);
+    if (st) return st;
+    if ((st = out_checks(qkv, dtype, row_stride, out, B, L, H, D, workspace, lay))) return st;
   }
   int st = hb_dense_prep(stream, qkv, dtype, row_stride, q_weight, k_weight, cos, sin, half, vmask, B, L, H, D, eps,
                          workspace, workspace_bytes);

@@ -420,6 +420,17 @@ extern "C" int hb_dit_qkv_proj(hipStream_t stream, const void* h, int dtype, int
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(HB_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (workspace_bytes < lay.total_bytes)
     return fail(HB_ERR_WORKSPACE, "workspace holds %zu bytes, needs %zu", workspace_bytes, lay.total_bytes);
+  {
+    const int64_t hb = rows_bytes(static_cast<int64_t>(B) * L, h_row_stride, E, 2);
+    const int64_t wb = rows_bytes(5 * HD, w_row_stride, E, 2), qb = static_cast<int64_t>(B) * L * 2 * HD * 2;
+    const int64_t sb = static_cast<int64_t>(lay.total_bytes);
+    const char* w = "qkv_proj";
+    if ((st = check_disjoint(w, "qq", qq, qb, "h", h, hb)) || (st = check_disjoint(w, "qq", qq, qb, "w_qkv", w_qkv, wb)) ||
+        (st = check_disjoint(w, "workspace", workspace, sb, "h", h, hb)) ||
+        (st = check_disjoint(w, "workspace", workspace, sb, "w_qkv", w_qkv, wb)) ||
+        (st = check_disjoint(w, "workspace", workspace, sb, "qq", qq, qb)))
+      return st;
+  }
 
   proj::Args a{};
   a.w = static_cast<const uint16_t*>(w_qkv);
@@ -468,6 +479,12 @@ extern "C" int hb_proj(hipStream_t stream, const void* x, int dtype, int64_t x_r
   if (!out) return fail(HB_ERR_NULL, "out must be non-NULL");
   if (reinterpret_cast<uintptr_t>(out) % 8 || out_row_stride < F || out_row_stride % 4)
     return fail(HB_ERR_STRIDE, "out must be 8-byte aligned with a row stride >= F and a multiple of 4");
+  {
+    const int64_t ob = rows_bytes(N, out_row_stride, F, 2);
+    if ((st = check_disjoint("proj", "out", out, ob, "x", x, rows_bytes(N, x_row_stride, K, 2))) ||
+        (st = check_disjoint("proj", "out", out, ob, "w", w, rows_bytes(F, w_row_stride, K, 2))))
+      return st;
+  }
   proj::Args a{};
   a.w = static_cast<const uint16_t*>(w);
   a.x = static_cast<const uint16_t*>(x);
@@ -519,6 +536,13 @@ extern "C" int hb_dense_attend_qq(hipStream_t stream, const void* qq, int dtype,
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(HB_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (workspace_bytes < lay.total_bytes)
     return fail(HB_ERR_WORKSPACE, "workspace holds %zu bytes, needs %zu", workspace_bytes, lay.total_bytes);
+  {
+    const int64_t HD = static_cast<int64_t>(H) * D, rows = static_cast<int64_t>(B) * L, ob = rows * HD * 2;
+    if ((st = check_disjoint("dense_attend_qq", "out", out, ob, "qq", qq, rows_bytes(rows, row_stride, 2 * HD, 2))) ||
+        (st = check_disjoint("dense_attend_qq", "out", out, ob, "workspace", workspace,
+                             static_cast<int64_t>(lay.total_bytes))))
+      return st;
+  }
   return launch_dense_attend_16bit(stream, dtype, qq, row_stride, 1, q_weight, k_weight, cos, sin, half, eps, lam, out, B,
                                    L, L, H, D, lay, workspace);
 }

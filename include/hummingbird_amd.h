@@ -28,6 +28,9 @@
  *     (sa3jax/dit.py:196-198, sa3jax/same_l.py:162). Element (b, n, c) sits at
  *     qkv[(b*N + n) * row_stride + c]; row_stride >= 5*H*D and a multiple of 8 elements; qkv 16-byte aligned.
  *   - The output `out` is dense (B, N, H*D) in `b n (h d)` order (sa3jax/dit.py:107-110), dtype = input dtype.
+ *   - Outputs and workspaces share no byte with the buffers the same call reads, nor with each other, as the
+ *     reference's functional calls never alias; an overlap is refused with HB_ERR_STRIDE before any launch. The
+ *     row-wise block entry points below state their exact rule (in-place hb_residual_dyt).
  *   - `lam` (H floats, or NULL for all ones) weights the second branch: out = A - lam[h] * B. lam = 1 is the
  *     reference's unweighted difference (sa3jax/dit.py:146, sa3jax/same_l.py:168).
  *   - Return value: HB_OK, or an HB_ERR_* code; hb_last_error() then describes the failure (thread-local).

@@ -202,6 +202,36 @@ def test_dit_block_entry_points_reject_before_any_launch(lib):
     assert res(gate=fake, gs=32) == 7 and res(local=fake + 2) == 7 and res(memory=-1) == 2
 
 
+def test_attention_outputs_that_overlap_their_inputs_are_refused(lib):
+    """The attention and projection entry points refuse an output or workspace whose bytes meet a buffer the same
+    call reads (HB_ERR_STRIDE), after every other check and before any launch (fake, never dereferenced, otherwise
+    valid addresses)."""
+    B, L, H, D = 1, 200, 2, 64
+    HD = H * D
+    qkv, w, tab = 0x100000, 0x400000, 0x500000
+    qkv_bytes = L * 5 * HD * 2                                           # 256000 bytes from qkv
+    need = lib.hb_dense_workspace_size(0, B, L, H, D)
+    ws, out = 0x1000000, 0x2000000                                       # far from everything
+
+    def dense(o=out, wsp=ws):
+        return lib.hb_dense_diffattn(None, qkv, 0, 5 * HD, w, w, tab, tab, 32, None, None, o, B, L, H, D, 1e-6, wsp,
+                                     need)
+    assert dense(o=qkv + qkv_bytes - 16) == 7                            # out's first row in qkv's last bytes
+    assert dense(wsp=qkv + 256 * (qkv_bytes // 256 - 1)) == 7            # workspace over qkv (256-byte aligned)
+    assert dense(o=ws + need - 8) == 7                                   # out over the workspace's end
+    assert "overlaps" in lib.hb_last_error().decode()
+    band = lambda o: lib.hb_band_diffattn(None, qkv, 0, 5 * HD, w, w, tab, tab, 32, 16, None, o, B, L, H, D, None, 0)  # noqa: E731
+    assert band(qkv + 5 * HD * 2 * 7) == 7                               # out inside qkv's rows
+    tneed = lib.hb_band_workspace_size(0, B, L, H, D, 32, 200)
+    tiled = lambda wsp: lib.hb_band_diffattn(None, qkv, 0, 5 * HD, w, w, tab, tab, 32, 200, None, out, B, L, H, D,  # noqa: E731
+                                             wsp, tneed)
+    assert tiled(out - 256 * 4) == 7 and tiled(qkv) == 7                 # the tiled path's workspace over out / qkv
+    cneed = lib.hb_cross_workspace_size(0, B, 257, H, D)
+    assert lib.hb_cross_prep(None, qkv, 0, 3 * HD, w, B, 257, H, D, 1e-6, qkv + 256 * 8, cneed) == 7
+    assert lib.hb_cross_attend(None, qkv, 0, 2 * HD, w, w, None, qkv + 64, B, L, 257, H, D, 1e-6, ws, cneed) == 7
+    assert lib.hb_proj(None, qkv, 0, 256, w, 256, qkv + 1024, 256, 64, 256, 256) == 7   # out over x
+
+
 def test_row_outputs_that_overlap_their_inputs_are_refused(lib):
     """Every row-wise entry point refuses an output that shares an element with a row input or with the other
     output, before any launch (HB_ERR_STRIDE; fake, never dereferenced addresses): partial overlaps within a row and
