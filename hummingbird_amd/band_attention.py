@@ -11,7 +11,7 @@ import weakref
 
 import torch
 
-from hummingbird_amd import _lib
+from hummingbird_amd import _lib, rotary
 from hummingbird_amd.dense_attention import (SUPPORTED_HEAD_DIMS, _f32, _require_gpu, _row_stride, dtype_code,
                                              rope_tables)
 
@@ -65,7 +65,9 @@ def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torc
     HIP kernel takes any window >= 0). `lam` `(H,)` optionally weights the second branch (default 1, the
     reference). `tables` optionally supplies `(cos, sin)` from `rope_tables(S, inv_freq)`. `workspace` optionally
     supplies the scratch that bf16 shapes outside the streaming kernel (window > 128 or head_dim 128) need:
-    `hb_band_workspace_size` bytes of uint8 on the same device; it is allocated here when absent.
+    `hb_band_workspace_size` bytes of uint8 on the same device; it is allocated here when absent. Any rotary
+    half-width `inv_freq.shape[0]` in `[0, head_dim / 2]` is taken; one that is not a multiple of 8 runs on a copy
+    of `qkv` with the q and k dims reordered (`hummingbird_amd.rotary`).
     """
     del rows, halo, sub, stack, interpret
     _require_gpu(qkv, "qkv")
@@ -93,6 +95,13 @@ def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torc
             cos, sin = (_f32(t, dev) for t in tables)
             if tuple(cos.shape) != (length, half) or tuple(sin.shape) != (length, half):
                 raise ValueError(f"tables must be (S, half) = ({length}, {half})")
+        if half % rotary.ALIGN:  # the kernels pair 8-dim groups: reorder the q and k dims (see rotary)
+            qkv = rotary.reorder_sections(qkv, num_heads, head_dim, half, (True, True, False, True, True))
+            rs = qkv.shape[-1]
+            qd, kd = (torch.cat([p[:1], rotary.reorder_dims(p[1:1 + head_dim], head_dim, half),
+                                 rotary.reorder_dims(p[1 + head_dim:], head_dim, half)]) for p in (qd, kd))
+            cos, sin = rotary.pad_tables(cos, sin, half)
+            half = rotary.aligned_half(half)
         cos_p, sin_p = cos.data_ptr(), sin.data_ptr()
     lam_p = 0
     if lam is not None:

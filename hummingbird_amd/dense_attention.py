@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import torch
 
-from hummingbird_amd import _lib
+from hummingbird_amd import _lib, rotary
 from hummingbird_amd._lib import HB_BF16, HB_F16, HB_F32
 
 SUPPORTED_HEAD_DIMS = (64, 128)
@@ -90,7 +90,9 @@ def dense_attention(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.T
     `interpret` are the TPU kernel's tiling knobs and are accepted and ignored (the HIP tiling is fixed).
     `lam` `(H,)` optionally weights the second branch (`A - lam * B`; default 1, the reference).
     `workspace` optionally supplies the scratch (`workspace_bytes(...)` bytes of uint8 on the same device).
-    Raises ValueError for unsupported shapes, like the reference does at trace time.
+    Any `half` in `[0, head_dim / 2]` is taken; one that is not a multiple of 8 runs on a copy of `qkv` with the q
+    and k dims reordered (`hummingbird_amd.rotary`). Raises ValueError for unsupported shapes, like the reference
+    does at trace time.
     """
     del rows, stack, interpret
     _require_gpu(qkv, "qkv")
@@ -115,6 +117,13 @@ def dense_attention(qkv: torch.Tensor, q_weight: torch.Tensor, k_weight: torch.T
         if tuple(cos.shape) != (length, half) or tuple(sin.shape) != (length, half):
             raise ValueError(f"cos/sin must be (L, half) = ({length}, {half}) from tables(), got {tuple(cos.shape)}")
         cos_p, sin_p = cos.data_ptr(), sin.data_ptr()
+    if half % rotary.ALIGN:  # the kernels pair 8-dim groups: reorder the q and k dims (see rotary)
+        qkv = rotary.reorder_sections(qkv, num_heads, head_dim, half, (True, True, False, True, True))
+        rs = qkv.shape[-1]
+        qw, kw = rotary.reorder_dims(qw, head_dim, half), rotary.reorder_dims(kw, head_dim, half)
+        cos, sin = rotary.pad_tables(cos, sin, half)
+        cos_p, sin_p = cos.data_ptr(), sin.data_ptr()
+        half = rotary.aligned_half(half)
     mask_p = 0
     if mask is not None:
         mask = _f32(mask, dev)

@@ -49,6 +49,8 @@ SMALL = [  # (B, S, H, D, window, half)
     (1, 1, 2, 64, 17, 32), (2, 17, 2, 64, 17, 16), (1, 100, 2, 64, 0, 32), (1, 100, 2, 64, 1, 32),
     (1, 300, 2, 64, 17, 16), (2, 300, 2, 64, 64, 32), (1, 700, 2, 64, 128, 32), (1, 333, 1, 64, 400, 32),
     (1, 260, 2, 128, 64, 64), (1, 200, 2, 64, 128, 0),
+    # rotary half-widths that are not a multiple of 8 (the wrapper reorders the q and k dims): ring and tiled
+    (1, 300, 2, 64, 17, 12), (1, 700, 2, 64, 128, 20), (1, 260, 2, 128, 64, 36), (1, 333, 1, 64, 200, 5),
 ]
 
 
@@ -101,7 +103,7 @@ def test_band_wide_window_equals_dense_attention():
 
 FP32_SHAPES = [  # (B, S, H, D, window, half)
     (1, 300, 2, 64, 17, 32), (1, 100, 2, 64, 0, 32), (2, 257, 2, 64, 64, 16), (1, 300, 2, 128, 17, 64),
-    (1, 50, 2, 64, 60, 0), (1, 1000, 1, 64, 128, 32),
+    (1, 50, 2, 64, 60, 0), (1, 1000, 1, 64, 128, 32), (1, 300, 2, 64, 17, 12), (1, 257, 2, 128, 64, 44),
 ]
 
 

@@ -47,6 +47,8 @@ SMALL = [  # (B, L, H, D, half)
     (1, 300, 2, 64, 0), (2, 216, 2, 128, 64), (1, 131, 2, 128, 32),
     # rotary half-widths whose RoPE partner group sits in the other half of a query row's lanes
     (1, 200, 2, 64, 24), (2, 100, 2, 64, 8), (1, 150, 2, 128, 40),
+    # rotary half-widths that are not a multiple of 8 (the wrapper reorders the q and k dims)
+    (1, 150, 2, 64, 12), (2, 129, 2, 64, 5), (1, 90, 2, 64, 31), (1, 100, 2, 128, 36),
 ]
 
 
@@ -120,6 +122,7 @@ def test_dense_lambda_linearity():
 FP32_SHAPES = [  # (B, L, H, D, half, ragged)
     (2, 1, 2, 64, 32, False), (2, 150, 2, 64, 32, False), (2, 216, 4, 64, 16, True), (1, 300, 2, 64, 0, False),
     (2, 129, 2, 128, 64, True), (1, 70, 3, 128, 32, False), (1, 100, 2, 64, 24, False), (1, 90, 2, 128, 56, True),
+    (1, 100, 2, 64, 20, True), (1, 90, 2, 128, 45, False),
 ]
 
 
