@@ -264,3 +264,23 @@ def test_band_errors_are_value_errors():
         ba.band_attention(qkv, n, n, torch.ones(16, device=DEV), 2, 64, -1)
     with pytest.raises(ValueError):
         ba.band_attention(qkv, n, n, torch.ones(40, device=DEV), 2, 64, 4)
+
+
+@pytest.mark.parametrize("half", [32, 12])
+def test_band_explicit_tables_equal_the_built_ones(half):
+    """`tables=(cos, sin)` from `rope_tables(S, inv_freq)` gives the output of the call that builds them itself, bit
+    for bit, also for a rotary width that is not a multiple of 8 (padded and reordered inside); tables of another
+    shape are refused."""
+    announce(f"band explicit tables half={half}")
+    inp = workloads.band_inputs(1, 500, 2, 64, 64, seed=77, half=half)
+    qkv = torch.from_numpy(inp["qkv"]).to(DEV, torch.bfloat16)
+    freq = torch.from_numpy(inp["inv_freq"]).to(DEV)
+    qn, kn = norm_t(inp["q_norm"]), norm_t(inp["k_norm"])
+    lam = torch.from_numpy(inp["lam"]).to(DEV)
+    built = ba.band_attention(qkv, qn, kn, freq, 2, 64, 64, lam=lam)
+    tabs = ba.rope_tables(500, freq)
+    given = ba.band_attention(qkv, qn, kn, freq, 2, 64, 64, lam=lam, tables=tabs)
+    torch.cuda.synchronize()
+    assert torch.equal(built, given)
+    with pytest.raises(ValueError):
+        ba.band_attention(qkv, qn, kn, freq, 2, 64, 64, tables=(tabs[0][:499], tabs[1][:499]))
