@@ -181,13 +181,13 @@ __global__ __launch_bounds__(256) void dense_prep(const uint16_t* __restrict__ q
 }
 
 // The key loop. Tile 0 has already been issued into stage A by the caller.
-template <int D, int QB, bool FAST>
+template <int D, int QB, int NW, bool FAST>
 __device__ __forceinline__ void dense_attend_loop(
-    const TileCopy<D>& issue, int L, int br0, uint16_t* sA, uint16_t* sB,
-    const u32x4 (&qf)[DenseTile<D, QB>::NB][DenseTile<D, QB>::NCT][D / 16],
-    f32x16 (&o)[DenseTile<D, QB>::NB][DenseTile<D, QB>::NCT][D / 32],
-    float (&lsum)[DenseTile<D, QB>::NB][DenseTile<D, QB>::NCT], float c) {
-  using T = DenseTile<D, QB>;
+    const TileCopy<D, NW>& issue, int L, int br0, uint16_t* sA, uint16_t* sB,
+    const u32x4 (&qf)[DenseTile<D, QB, NW>::NB][DenseTile<D, QB, NW>::NCT][D / 16],
+    f32x16 (&o)[DenseTile<D, QB, NW>::NB][DenseTile<D, QB, NW>::NCT][D / 32],
+    float (&lsum)[DenseTile<D, QB, NW>::NB][DenseTile<D, QB, NW>::NCT], float c) {
+  using T = DenseTile<D, QB, NW>;
   constexpr int NB = T::NB, NCT = T::NCT;
   const int tid = threadIdx.x;
   const int nkt = (L + 63) / 64;
@@ -253,7 +253,7 @@ __device__ __forceinline__ void dense_attend_loop(
 // and after the rotation, bf16 after the scale. The rotary width is a template parameter so that the partner of every dim is a
 // fixed register. Rows at or past L are prepared from row L - 1 (the caller clamps `row`); their outputs are
 // never stored, and real rows keep the logits within the softmax plan's bound.
-template <class IO, int D, int H8>
+template <class IO, int D, int H8, bool STREAM>
 __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, const float* __restrict__ qw,
                                            const float* __restrict__ cs, const float* __restrict__ sn, float eps,
                                            float qscale, u32x4 (&out)[D / 8]) {
@@ -262,7 +262,7 @@ __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, con
   for (int c = 0; c < D / 8; ++c) raw[c] = ld16(row + 8 * c);
   float cv[8 * H8 + 1], sv[8 * H8 + 1];
 #pragma unroll
-  for (int j4 = 0; j4 < 2 * H8; ++j4) {
+  for (int j4 = 0; j4 < (STREAM ? 0 : 2 * H8); ++j4) {  // the streamed form loads its slices chunk by chunk
     const f32x4 c4 = *reinterpret_cast<const f32x4*>(cs + 4 * j4);
     const f32x4 s4 = *reinterpret_cast<const f32x4*>(sn + 4 * j4);
 #pragma unroll
@@ -270,6 +270,54 @@ __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, con
       cv[4 * j4 + e] = c4[e];
       sv[4 * j4 + e] = s4[e];
     }
+  }
+  if constexpr (STREAM) {
+    // The same arithmetic chunk pair by chunk pair, so that the whole fp32 row and its tables are never live at
+    // once (head_dim 128 with two waves per SIMD, at most 256 registers each).
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+      float t[8];
+      IO::unpack8(raw[c], t);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = __fmaf_rn(t[j], t[j], ss);
+    }
+    const float inv = rsqrtf(ss / static_cast<float>(D) + eps);
+    auto normed = [&](int c, float (&y)[8]) {
+      IO::unpack8(raw[c], y);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = IO::round((y[j] * inv) * qw[8 * c + j]);
+    };
+    auto emit = [&](int c, const float (&y)[8]) {
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = y[j] * qscale;
+      out[c] = pack8(o);
+    };
+#pragma unroll
+    for (int c = 0; c < H8; ++c) {  // chunk c rotates with chunk c + H8 (dims d and d + half)
+      float y1[8], y2[8], r1[8], r2[8];
+      normed(c, y1);
+      normed(c + H8, y2);
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(cs + 8 * c), c1 = *reinterpret_cast<const f32x4*>(cs + 8 * c + 4);
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(sn + 8 * c), s1 = *reinterpret_cast<const f32x4*>(sn + 8 * c + 4);
+      const float cvv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+      const float svv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        r1[j] = IO::round(y1[j] * cvv[j] + (-y2[j]) * svv[j]);
+        r2[j] = IO::round(y2[j] * cvv[j] + y1[j] * svv[j]);
+      }
+      emit(c, r1);
+      emit(c + H8, r2);
+    }
+#pragma unroll
+    for (int c = 2 * H8; c < D / 8; ++c) {
+      float y[8];
+      normed(c, y);
+      emit(c, y);
+    }
+    return;
   }
   float y[D];
   float ss = 0.f;
@@ -302,24 +350,25 @@ __device__ __forceinline__ void prep_q_row(const uint16_t* __restrict__ row, con
 // the 64-query form runs three workgroups per CU.
 // IO: the element type of qkv and out (bf16 or half); the attention operands are bf16 either way. QB: queries per
 // workgroup; the 64-query form runs three workgroups per CU.
-template <class IO, int D, int QB>
-__global__ __launch_bounds__(256, D == 64 ? (QB == 64 ? 3 : 2) : 1) void dense_attend(
+template <class IO, int D, int QB, int NW>
+__global__ __launch_bounds__(64 * NW, D == 64 ? (QB == 64 ? 3 : 2) : 1) void dense_attend(
     const uint16_t* __restrict__ qkv, int64_t rs, int sqd, const float* __restrict__ cosT,
     const float* __restrict__ sinT, int half, float eps, const uint16_t* __restrict__ ws, int64_t region, int B,
     int L, int Lp, int Lk, int Lkp, int H, const float* __restrict__ qw, const float* __restrict__ kw,
     const float* __restrict__ lam, uint16_t* __restrict__ out) {
-  using T = DenseTile<D, QB>;
+  using T = DenseTile<D, QB, NW>;
   constexpr int NB = T::NB, NCT = T::NCT;
-  // Stages A and B of the K/V tiles; the epilogue reuses the first 32 KB as its exchange buffer.
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * T::STAGE];
+  // Stages A and B of the K/V tiles; the epilogue reuses the array as its exchange buffer.
+  __shared__ __attribute__((aligned(16))) uint16_t smem[T::SMEM_ELEMS];
   const int nqb = Lp / QB;
   const int tile = xcd_remap(blockIdx.x, B * H * nqb);
   const int qb = tile % nqb, bh = tile / nqb, h = bh % H, b = bh / H;
   const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
-  const int br0 = T::SPLIT ? wave >> 1 : 0;                                 // first branch of this wave
-  const int q0 = qb * QB + (T::SPLIT ? (wave & 1) * 32 * NCT : wave * 32);  // first query of this wave
+  const int br0 = T::SPLIT ? wave / (NW / 2) : 0;                                 // first branch of this wave
+  const int q0 = qb * QB + (T::SPLIT ? (wave % (NW / 2)) * 32 * NCT : wave * 32);  // first query of this wave
   const int64_t rowbase = static_cast<int64_t>(bh) * Lkp;
 
+  constexpr bool kStream = D == 128 && NW == 8;  // the query prologue in the register budget of two waves per SIMD
   // Launch-uniform choice between the max-free and the running-max softmax (see the file comment).
   const SoftmaxPlan plan = dense_plan<D>(qw, kw);
 
@@ -339,20 +388,20 @@ __global__ __launch_bounds__(256, D == 64 ? (QB == 64 ? 3 : 2) : 1) void dense_a
     const float* sn = sinT + static_cast<int64_t>(qc) * half;
     u32x4 whole[D / 8];
     switch (half / 8) {  // half % 8 == 0 and half <= D / 2 are checked on the host
-      case 0: prep_q_row<IO, D, 0>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 1: prep_q_row<IO, D, 1>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 2: prep_q_row<IO, D, 2>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-      case 3: prep_q_row<IO, D, 3>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 0: prep_q_row<IO, D, 0, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 1: prep_q_row<IO, D, 1, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 2: prep_q_row<IO, D, 2, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+      case 3: prep_q_row<IO, D, 3, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
       default:
         if constexpr (D == 64) {
-          prep_q_row<IO, D, 4>(row, qw, cs, sn, eps, plan.qscale, whole);
+          prep_q_row<IO, D, 4, kStream>(row, qw, cs, sn, eps, plan.qscale, whole);
         } else {
           switch (half / 8) {
-            case 4: prep_q_row<IO, D, 4>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 5: prep_q_row<IO, D, 5>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 6: prep_q_row<IO, D, 6>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-            case 7: prep_q_row<IO, D, 7>(row, qw, cs, sn, eps, plan.qscale, whole); break;
-            default: prep_q_row<IO, D, 8>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 4: prep_q_row<IO, D, 4, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 5: prep_q_row<IO, D, 5, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 6: prep_q_row<IO, D, 6, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            case 7: prep_q_row<IO, D, 7, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
+            default: prep_q_row<IO, D, 8, kStream>(row, qw, cs, sn, eps, plan.qscale, whole); break;
           }
         }
     }
@@ -384,17 +433,17 @@ __global__ __launch_bounds__(256, D == 64 ? (QB == 64 ? 3 : 2) : 1) void dense_a
       for (int dt = 0; dt < D / 32; ++dt) o[bi][ct][dt] = f32x16{};
     }
 
-  const TileCopy<D> copy(ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D);
+  const TileCopy<D, NW> copy(ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D);
   copy(0, lds_addr(smem));
   if (plan.fast)
-    dense_attend_loop<D, QB, true>(copy, Lk, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
+    dense_attend_loop<D, QB, NW, true>(copy, Lk, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
   else
-    dense_attend_loop<D, QB, false>(copy, Lk, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
+    dense_attend_loop<D, QB, NW, false>(copy, Lk, br0, smem, smem + T::STAGE, qf, o, lsum, plan.c);
 
   // Both stages are free once every wave is past its last tile; the exchange reuses them.
-  static_assert(2 * NCT * (D / 32) * 16 * 64 * 4 <= 2 * T::STAGE * 2, "exchange buffer exceeds the two stages");
+  static_assert(T::XBUF_BYTES <= T::SMEM_ELEMS * 2, "exchange buffer exceeds the workgroup's LDS");
   if constexpr (T::SPLIT) __syncthreads();
-  store_diff_split<D, QB, IO>(out, b, L, H, h, q0, br0, lam ? lam[h] : 1.f, o, lsum, smem);
+  store_diff_split<D, QB, IO, NW>(out, b, L, H, h, q0, br0, lam ? lam[h] : 1.f, o, lsum, smem);
 }
 
 __global__ void rope_tables_kernel(const float* __restrict__ inv_freq, int half, int length, float* __restrict__ cosT,
@@ -489,14 +538,19 @@ int launch_dense_attend_16bit(hipStream_t stream, int dtype, const void* q, int6
   const int64_t ncu = device_cus();
   if (D == 64 && blocks128 > ncu && 2 * blocks128 <= 3 * ncu) {
     const int nblocks = B * H * (Lp / 64);
-    auto kernel = f16 ? dense_attend<F16Io, 64, 64> : dense_attend<Bf16Io, 64, 64>;
+    auto kernel = f16 ? dense_attend<F16Io, 64, 64, 4> : dense_attend<Bf16Io, 64, 64, 4>;
     hipLaunchKernelGGL(kernel, dim3(nblocks), dim3(DenseTile<64, 64>::NT), 0, stream, x, rs, sqd, cos, sin, half, eps,
                        ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw, lam, o);
   } else {
-    auto kernel = D == 64 ? (f16 ? dense_attend<F16Io, 64, 128> : dense_attend<Bf16Io, 64, 128>)
-                          : (f16 ? dense_attend<F16Io, 128, 128> : dense_attend<Bf16Io, 128, 128>);
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks128)), dim3(256), 0, stream, x, rs, sqd, cos, sin,
-                       half, eps, ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw, lam, o);
+    // head_dim 128: 8 waves of one branch each (two per SIMD) once the grid fills the GPU; below that the 4-wave
+    // form, whose fixed part per workgroup is smaller (measured: 7 % faster at L = 1292 and 2584, 17 % slower at
+    // L = 216 with 48 workgroups)
+    const bool w8 = D == 128 && blocks128 >= ncu;
+    auto kernel = D == 64 ? (f16 ? dense_attend<F16Io, 64, 128, 4> : dense_attend<Bf16Io, 64, 128, 4>)
+                  : w8    ? (f16 ? dense_attend<F16Io, 128, 128, 8> : dense_attend<Bf16Io, 128, 128, 8>)
+                          : (f16 ? dense_attend<F16Io, 128, 128, 4> : dense_attend<Bf16Io, 128, 128, 4>);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks128)), dim3(w8 ? 512 : 256), 0, stream, x, rs, sqd,
+                       cos, sin, half, eps, ws, lay.region_elems, B, L, Lp, Lk, Lkp, H, qw, kw, lam, o);
   }
   return launch_status("dense_attend");
 }

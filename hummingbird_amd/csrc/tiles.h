@@ -37,28 +37,36 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   else return row * RL + 8 * (chunk ^ (row & 15));
 }
 
-// Attention tiling: a workgroup of 4 waves attends QB queries (128, or 64 for grids too small to fill the GPU).
-// D = 64: each wave owns one differential branch of QB / 2 queries (QB / 64 MFMA column tiles; at QB = 128 every
-// K fragment read from LDS feeds two MFMAs while a wave's registers still fit two waves per SIMD); waves 0-1 run
-// branch 1 (q, k) and waves 2-3 branch 2 (q_diff, k_diff), and the second pair hands its normalised result to the
-// first through LDS at the end. D = 128 (QB = 128 only): each wave owns both branches of 32 queries.
-template <int D, int QB = 128>
+// Attention tiling: a workgroup of NW waves attends QB queries.
+//   - Split layouts (D = 64 with 4 waves; D = 128 with 8 waves): each wave owns one differential branch of
+//     32 * NCT queries; the first NW / 2 waves run branch 1 (q, k), the others branch 2 (q_diff, k_diff), and each
+//     branch-2 wave hands its normalised result to the branch-1 wave of the same queries through LDS at the end.
+//     D = 64: QB = 128 (two MFMA column tiles per wave, so every K fragment read from LDS feeds two MFMAs while a
+//     wave's registers still fit two waves per SIMD) or 64 for grids too small to fill the GPU. D = 128: QB = 128
+//     over 8 waves, one column tile each, so two waves share each SIMD in the one workgroup per CU that the 96 KB
+//     of K/V stages allow.
+//   - D = 128 with 4 waves (the tiled band kernels): each wave owns both branches of 32 queries.
+template <int D, int QB = 128, int NW = 4>
 struct DenseTile {
-  static_assert(QB == 128 || (D == 64 && QB == 64), "64-query workgroups exist for head_dim 64 only");
-  static constexpr bool SPLIT = D == 64;          // one branch per wave
-  static constexpr int NB = SPLIT ? 1 : 2;         // branches per wave
-  static constexpr int NCT = SPLIT ? QB / 64 : 1;  // 32-query column tiles per wave
-  static constexpr int NT = 256;            // threads per workgroup
+  static_assert((NW == 4 && (QB == 128 || (D == 64 && QB == 64))) || (NW == 8 && D == 128 && QB == 128),
+                "tilings: D = 64 with 4 waves (QB 128 or 64), D = 128 with 4 or 8 waves (QB 128)");
+  static constexpr bool SPLIT = D == 64 || NW == 8;         // one branch per wave
+  static constexpr int NB = SPLIT ? 1 : 2;                   // branches per wave
+  static constexpr int NCT = SPLIT ? QB / (16 * NW) : 1;     // 32-query column tiles per wave
+  static constexpr int NT = 64 * NW;                         // threads per workgroup
   static constexpr int K_ELEMS = 64 * D;     // one tensor of a 64-key tile: K, K_diff [key][d]; V^T [d][pos]
   static constexpr int STAGE = 3 * K_ELEMS;  // K, K_diff, V^T of one 64-key tile, swizzled rows
   static constexpr int BPT = 64 * D * 2 / 1024;  // 1 KB blocks per tensor of a 64-key tile
-  static constexpr int NBLK = 3 * BPT;            // blocks per tile (a multiple of the 4 waves)
+  static constexpr int NBLK = 3 * BPT;            // blocks per tile (a multiple of the waves)
+  // the split epilogue's hand-over (fp32 accumulators of every branch-2 wave), and the LDS a workgroup declares
+  static constexpr int XBUF_BYTES = SPLIT ? (NW / 2) * NCT * (D / 32) * 16 * 64 * 4 : 0;
+  static constexpr int SMEM_ELEMS = 2 * STAGE > XBUF_BYTES / 2 ? 2 * STAGE : XBUF_BYTES / 2;
 };
 
 // Copies 64-key tile t of K, K_diff and V'^T from the workspace straight into an LDS stage (global_load_lds, no
 // registers). Each wave copies 1 KB blocks: lane i lands at byte 16 i of its block, so it fetches the chunk that
 // the swizzled layout puts there.
-template <int D>
+template <int D, int NW = 4>
 struct TileCopy {
   const uint16_t* Kb;
   const uint16_t* Kdb;
@@ -85,8 +93,8 @@ struct TileCopy {
       const uint16_t* base = (tsr == 0 ? Kb : tsr == 1 ? Kdb : Vb) + static_cast<int64_t>(t) * 64 * D;
       const uint32_t off = tsr < 2 && D == 128 ? off128 : off64;
 #pragma unroll
-      for (int u = 0; u < T::BPT / 4; ++u)  // blocks wv, wv + 4, ...
-        lds_dma16(base, off + u * 4096, stage + 2 * tsr * T::K_ELEMS + (wv + 4 * u) * 1024);
+      for (int u = 0; u < T::BPT / NW; ++u)  // blocks wv, wv + NW, ...
+        lds_dma16(base, off + u * NW * 1024, stage + 2 * tsr * T::K_ELEMS + (wv + NW * u) * 1024);
     }
   }
 };
@@ -96,19 +104,18 @@ struct TileCopy {
 // D = 64: the branch-2 waves publish lam * O2 / l2 (rounded per element) through LDS (`xbuf_mem`, at least
 // 32 KB, free of tile reads: the caller has passed a barrier after its last tile) and the branch-1 waves
 // subtract it from O1 / l1; D = 128: each wave holds both branches. Every lane of the workgroup must call it.
-template <int D, int QB = 128, class IO = Bf16Io>
-__device__ __forceinline__ void store_diff_split(uint16_t* __restrict__ out, int64_t b, int N, int H, int h, int q0w,
-                                                 int br0, float lamh,
-                                                 const f32x16 (&o)[DenseTile<D, QB>::NB][DenseTile<D, QB>::NCT][D / 32],
-                                                 const float (&lsum)[DenseTile<D, QB>::NB][DenseTile<D, QB>::NCT],
-                                                 uint16_t* xbuf_mem) {
-  using T = DenseTile<D, QB>;
+template <int D, int QB = 128, class IO = Bf16Io, int NW = 4>
+__device__ __forceinline__ void store_diff_split(
+    uint16_t* __restrict__ out, int64_t b, int N, int H, int h, int q0w, int br0, float lamh,
+    const f32x16 (&o)[DenseTile<D, QB, NW>::NB][DenseTile<D, QB, NW>::NCT][D / 32],
+    const float (&lsum)[DenseTile<D, QB, NW>::NB][DenseTile<D, QB, NW>::NCT], uint16_t* xbuf_mem) {
+  using T = DenseTile<D, QB, NW>;
   constexpr int NCT = T::NCT;
   const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
   const int64_t HD = static_cast<int64_t>(H) * D;
   if constexpr (T::SPLIT) {
     float* xbuf = reinterpret_cast<float*>(xbuf_mem);  // 2 query halves x NCT x D/32 x 16 registers x 64 lanes
-    const int slot0 = (wave & 1) * NCT * (D / 32) * 16;
+    const int slot0 = (wave % (NW / 2)) * NCT * (D / 32) * 16;
     if (br0 == 1) {
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
