@@ -534,10 +534,11 @@ int launch_dense_attend_16bit(hipStream_t stream, int dtype, const void* q, int6
   // two while most run one; 64-query workgroups (three per CU) spread the same work more evenly (measured: 6 %
   // faster at 288 workgroups on 256 CUs; slower at exactly one per CU and at nearly two, where they cost more per
   // query than they gain in balance). Just past two per CU (a nearly empty second round of 128-query workgroups)
-  // they win again: 3 % at 528 workgroups on 256 CUs (B = 2, L = 1292, H = 24).
+  // they win again: 3 % at 528 workgroups on 256 CUs (B = 2, L = 1292, H = 24). And on grids of at most half a
+  // 128-query workgroup per CU they halve the work of each busy CU: 9.8 against 11.4 us at B = 1, L = 216, H = 24.
   const int64_t blocks128 = static_cast<int64_t>(B) * H * (Lp / 128);
   const int64_t ncu = device_cus();
-  const bool spread = (blocks128 > ncu && 2 * blocks128 <= 3 * ncu) ||
+  const bool spread = 2 * blocks128 <= ncu || (blocks128 > ncu && 2 * blocks128 <= 3 * ncu) ||
                       (blocks128 > 2 * ncu && 8 * blocks128 <= 17 * ncu);
   if (D == 64 && spread) {
     const int nblocks = B * H * (Lp / 64);
