@@ -262,6 +262,34 @@ def test_row_outputs_that_overlap_their_inputs_are_refused(lib):
     assert "overlaps" in lib.hb_last_error().decode()
 
 
+
+def test_row_overlap_check_matches_brute_force(lib):
+    """The row-overlap test behind every row-wise entry point, against a byte-by-byte intersection of the rows on
+    random layouts (hb_dyt, bf16 rows of 8 elements; fake, never dereferenced addresses). Equal row strides are
+    decided exactly, so interleaved rows that share no byte pass the check (and reach the launch, which fails here
+    without a GPU); unequal strides are refused whenever the two address ranges meet."""
+    import random
+
+    rng = random.Random(11)
+    C, esize, base = 8, 2, 0x100000
+    for _ in range(400):
+        N = rng.randint(1, 6)
+        xs, os_ = rng.choice([8, 16, 24, 32]), rng.choice([8, 16, 24, 32])
+        if rng.random() < 0.6:
+            os_ = xs
+        x = base + 16 * rng.randint(0, 24)
+        out = base + 16 * rng.randint(0, 24)
+        rows = lambda p, s: {p + i * s * esize + k for i in range(N) for k in range(C * esize)}  # noqa: E731
+        shared = bool(rows(x, xs) & rows(out, os_))
+        st = lib.hb_dyt(None, x, 0, xs, base + 0x80000, out, os_, N, C)
+        if shared:
+            assert st == 7, (N, xs, os_, x - base, out - base)
+        elif xs == os_:
+            assert st != 7, (N, xs, os_, x - base, out - base, lib.hb_last_error().decode())
+        else:
+            x_end, o_end = x + ((N - 1) * xs + C) * esize, out + ((N - 1) * os_ + C) * esize
+            assert (st == 7) == (x < o_end and out < x_end), (N, xs, os_, x - base, out - base)
+
 def test_residual_rms_rejects_before_any_launch(lib):
     fake = 0x100000
     call = lambda **kw: lib.hb_residual_rms(  # noqa: E731
