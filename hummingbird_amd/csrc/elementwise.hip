@@ -80,51 +80,6 @@ __global__ __launch_bounds__(256) void dyt_kernel(const T* __restrict__ x, int64
 // times a bf16 array is a bf16 multiply in JAX) and the product held in it before the sine.
 // `bias` (2F values of the compute dtype, or null): the glu_proj layer's bias, added to the GEMM output in the
 // compute dtype first (same_l._linear: the matmul, then the bias add, each held in the compute dtype).
-// One 16-byte output chunk: out_row[c0 ..] = value * act(gate) for the value and gate chunks at row[c0 ..] and
-// row[F + c0 ..].
-template <typename T, bool SINE>
-__device__ __forceinline__ void glu_chunk(const T* __restrict__ row, const float* __restrict__ bias, int F, int c0,
-                                          T* __restrict__ out_row) {
-  constexpr int V = Vec<T>::N;
-  float val[V], g[V];
-  Vec<T>::load(row + c0, val);
-  Vec<T>::load(row + F + c0, g);
-  if (bias) {
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      val[i] = Vec<T>::round(val[i] + bias[c0 + i]);
-      g[i] = Vec<T>::round(g[i] + bias[F + c0 + i]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < V; ++i) {
-    float act;
-    if constexpr (SINE) {
-      const float t = Vec<T>::round(Vec<T>::round(static_cast<float>(M_PI)) * g[i]);
-      if constexpr (Vec<T>::kHwSine) {
-        // bf16: Cody-Waite reduction of t by 2 pi = C1 + C2 (C1 = 6.28125 has 8 significant bits, so k * C1 is
-        // exact for |k| < 2^16), then the hardware sine (v_sin_f32, argument in revolutions) of the remainder,
-        // |rev| <= 1/2. Its error is far inside the bf16 rounding of the result. Larger |t| take the library sine.
-        constexpr float inv2pi = static_cast<float>(0.5 / M_PI);
-        if (__builtin_expect(fabsf(t) > 65536.f, 0)) {
-          act = sinf(t);
-        } else {
-          const float k = rintf(t * inv2pi);
-          const float r = __fmaf_rn(-k, 1.9353071795864769e-3f, __fmaf_rn(-k, 6.28125f, t));
-          act = __builtin_amdgcn_sinf(r * inv2pi);
-        }
-      } else {
-        act = sinf(t);
-      }
-    } else {
-      act = g[i] * Vec<T>::round(__builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * g[i])));
-    }
-    val[i] = val[i] * Vec<T>::round(act);
-  }
-  Vec<T>::store(out_row + c0, val);
-}
-
-// Grid-stride form: thread i takes chunk i of the flattened (row, chunk) range, then every gridDim * 256-th.
 template <typename T, bool SINE>
 __global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ proj, int64_t ps,
                                                   const float* __restrict__ bias, T* __restrict__ out, int64_t os,
@@ -135,21 +90,43 @@ __global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ proj, in
        i += static_cast<int64_t>(gridDim.x) * 256) {
     const int64_t n = i / chunks;
     const int c0 = static_cast<int>(i - n * chunks) * V;
-    glu_chunk<T, SINE>(proj + n * ps, bias, F, c0, out + n * os);
+    float val[V], g[V];
+    Vec<T>::load(proj + n * ps + c0, val);
+    Vec<T>::load(proj + n * ps + F + c0, g);
+    if (bias) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        val[i] = Vec<T>::round(val[i] + bias[c0 + i]);
+        g[i] = Vec<T>::round(g[i] + bias[F + c0 + i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      float act;
+      if constexpr (SINE) {
+        const float t = Vec<T>::round(Vec<T>::round(static_cast<float>(M_PI)) * g[i]);
+        if constexpr (Vec<T>::kHwSine) {
+          // bf16: Cody-Waite reduction of t by 2 pi = C1 + C2 (C1 = 6.28125 has 8 significant bits, so k * C1 is
+          // exact for |k| < 2^16), then the hardware sine (v_sin_f32, argument in revolutions) of the remainder,
+          // |rev| <= 1/2. Its error is far inside the bf16 rounding of the result. Larger |t| take the library sine.
+          constexpr float inv2pi = static_cast<float>(0.5 / M_PI);
+          if (__builtin_expect(fabsf(t) > 65536.f, 0)) {
+            act = sinf(t);
+          } else {
+            const float k = rintf(t * inv2pi);
+            const float r = __fmaf_rn(-k, 1.9353071795864769e-3f, __fmaf_rn(-k, 6.28125f, t));
+            act = __builtin_amdgcn_sinf(r * inv2pi);
+          }
+        } else {
+          act = sinf(t);
+        }
+      } else {
+        act = g[i] * Vec<T>::round(__builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * g[i])));
+      }
+      val[i] = val[i] * Vec<T>::round(act);
+    }
+    Vec<T>::store(out + n * os + c0, val);
   }
-}
-
-// Row-walk form: one wave per (64-chunk column group cg, row slot r0), lane l taking chunk 64 cg + l of rows r0,
-// r0 + R, r0 + 2R, ... (`ncg` groups, R slots).
-template <typename T, bool SINE>
-__global__ __launch_bounds__(64) void glu_rows_kernel(const T* __restrict__ proj, int64_t ps,
-                                                      const float* __restrict__ bias, T* __restrict__ out,
-                                                      int64_t os, int64_t N, int F, int ncg, int R) {
-  constexpr int V = Vec<T>::N;
-  const int cg = static_cast<int>(blockIdx.x % ncg), r0 = static_cast<int>(blockIdx.x / ncg);
-  const int c = cg * 64 + static_cast<int>(threadIdx.x);
-  if (c >= F / V) return;
-  for (int64_t n = r0; n < N; n += R) glu_chunk<T, SINE>(proj + n * ps, bias, F, c * V, out + n * os);
 }
 
 // The block's residual adds with what surrounds them (same_l.py:191-192): out_h = h + (x + bias), the projection's
@@ -263,42 +240,34 @@ int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_str
                              static_cast<int64_t>(2) * F, N, dtype == HB_F32 ? 4 : 2, false)))
     return st;
   const int chunks = F / (dtype == HB_F32 ? 4 : 8);
-  // bf16 and half rows of 3072 to 6144 outputs over at least 16384 rows (the reference's decoder, F = 4608 over
-  // 23086 frames) take the row-walk form: measured 11-20 % faster there (125.7 against 152.6 us at 23086 x 4608),
-  // and 5-50 % slower than the grid-stride form at F = 1536, at F = 8192 and over fewer rows.
-  const bool rows = dtype != HB_F32 && F >= 3072 && F <= 6144 && N >= 16384;
-  const int ncg = (chunks + 63) / 64;
-  const int64_t slots = 32 * static_cast<int64_t>(device_cus()) / ncg;
-  const int R = static_cast<int>(N < slots ? N : (slots > 0 ? slots : 1));
-  auto launch = [&](auto* p, auto* o, auto flat_kernel, auto rows_kernel) {
-    if (rows)
-      hipLaunchKernelGGL(rows_kernel, dim3(static_cast<unsigned>(static_cast<int64_t>(ncg) * R)), dim3(64), 0, stream,
-                         p, proj_row_stride, bias, o, out_row_stride, N, F, ncg, R);
-    else
-      hipLaunchKernelGGL(flat_kernel, row_grid(N, chunks), dim3(256), 0, stream, p, proj_row_stride, bias, o,
-                         out_row_stride, N, F);
-  };
+  const dim3 grid = row_grid(N, chunks);
   if (dtype == HB_F16) {
     const _Float16* p = static_cast<const _Float16*>(proj);
     _Float16* o = static_cast<_Float16*>(out);
     if (sinusoidal)
-      launch(p, o, ew::glu_kernel<_Float16, true>, ew::glu_rows_kernel<_Float16, true>);
+      hipLaunchKernelGGL((ew::glu_kernel<_Float16, true>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
     else
-      launch(p, o, ew::glu_kernel<_Float16, false>, ew::glu_rows_kernel<_Float16, false>);
+      hipLaunchKernelGGL((ew::glu_kernel<_Float16, false>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
   } else if (dtype == HB_BF16) {
     const uint16_t* p = static_cast<const uint16_t*>(proj);
     uint16_t* o = static_cast<uint16_t*>(out);
     if (sinusoidal)
-      launch(p, o, ew::glu_kernel<uint16_t, true>, ew::glu_rows_kernel<uint16_t, true>);
+      hipLaunchKernelGGL((ew::glu_kernel<uint16_t, true>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
     else
-      launch(p, o, ew::glu_kernel<uint16_t, false>, ew::glu_rows_kernel<uint16_t, false>);
+      hipLaunchKernelGGL((ew::glu_kernel<uint16_t, false>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
   } else {
     const float* p = static_cast<const float*>(proj);
     float* o = static_cast<float*>(out);
     if (sinusoidal)
-      launch(p, o, ew::glu_kernel<float, true>, ew::glu_rows_kernel<float, true>);
+      hipLaunchKernelGGL((ew::glu_kernel<float, true>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
     else
-      launch(p, o, ew::glu_kernel<float, false>, ew::glu_rows_kernel<float, false>);
+      hipLaunchKernelGGL((ew::glu_kernel<float, false>), grid, dim3(256), 0, stream, p, proj_row_stride, bias,
+                         o, out_row_stride, N, F);
   }
   return launched("glu");
 }

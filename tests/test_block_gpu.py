@@ -109,36 +109,6 @@ def test_glu_with_bias_vs_oracle(sine, dtype):
         assert_within_one_bf16_step(got, ref, "glu with bias")
 
 
-
-@pytest.mark.parametrize("case", [(3072, False, False, "bf16"), (4608, True, True, "bf16"), (6144, False, True, "f16")],
-                         ids=["F3072-silu-bf16", "F4608-sine-bias-bf16", "F6144-silu-bias-f16"])
-def test_glu_row_walk_equals_grid_stride(case):
-    """hb_glu runs 16-bit rows of 3072 to 6144 outputs over at least 16384 rows (the reference's decoder shape) in
-    its row-walk form and fewer rows in its grid-stride form: the same rows give bit-identical outputs either way
-    (16400 rows at once against slices of 8200 rows, padded row stride), and the oracle agrees on the first and
-    last 100 rows."""
-    f, sine, with_bias, dtype = case
-    n = 16400
-    announce(f"glu row walk F={f} sine={sine} bias={with_bias} {dtype}")
-    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
-    gen = torch.Generator(device=DEV).manual_seed(f)
-    wide = (2 * torch.randn((n, 2 * f + 64), device=DEV, generator=gen)).to(tdt)
-    pt = wide[:, : 2 * f]
-    bias = (0.5 * torch.randn(2 * f, device=DEV, generator=gen)).to(tdt) if with_bias else None
-    got = elementwise.glu(pt, sine, bias=bias)
-    parts = torch.cat([elementwise.glu(pt[i:i + n // 2], sine, bias=bias) for i in (0, n // 2)])
-    assert torch.equal(got, parts)
-    for rows in (slice(0, 100), slice(n - 100, n)):
-        x = pt[rows].float().cpu().numpy().astype(np.float64)
-        if with_bias:
-            x = oblock.cast(x + bias.float().cpu().numpy(), "bf16" if dtype == "bf16" else "fp16")
-        ref = oblock.glu(x, sine, "bf16" if dtype == "bf16" else "fp16")
-        g = got[rows].float().cpu().numpy()
-        if dtype == "bf16":
-            assert_within_one_bf16_step(g, ref, f"glu row walk F={f}")
-        else:
-            assert np.abs(g - ref).max() <= 2.0 ** -9 * max(1.0, float(np.abs(ref).max())), f"glu row walk F={f}"
-
 @pytest.mark.parametrize("scale", [40.0, 400.0, 30000.0], ids=["gate40", "gate400", "gate30000"])
 def test_glu_sine_large_gates_vs_oracle(scale):
     """bf16 sine gates far outside the usual range: pi * gate reaches ~500 rad (scale 40) and ~5000 rad (scale
