@@ -7,9 +7,9 @@
 // One workgroup of 8 waves per CU walks a contiguous run of 64-query steps along the sequence of one
 // (batch, head). The keys step j can reach, [64j - 64C, 64j + 64 + 64C) with C = ceil(w / 64), live in an LDS
 // ring of 2C + 1 tiles of 64 keys, each holding K and K_diff after DyT (same_l.py:58-69) and rotate-half RoPE
-// (same_l.py:92-100) rounded once to bf16, and the raw V rows. A step retires the oldest tile and adds one,
-// so every key is prepared once per run (the reference's kernel prepares each key block three times, once per
-// halo; band_attention.py:155-169).
+// (same_l.py:92-100) rounded once to bf16, and the raw V rows (K and K_diff in one ring, V in another). A step
+// retires the oldest tile and adds one, so every key is prepared once per run (the reference's kernel prepares
+// each key block three times, once per halo; band_attention.py:155-169).
 //
 // The waves have two roles, one of each on every SIMD, so that one role's VALU work runs while the other
 // waits on LDS, memory or the matrix core:
@@ -21,7 +21,9 @@
 //     bf16 cast (same_l.py:168-169).
 //   - prep waves 4-7: meanwhile load and prepare the next step's key tile (k, k_diff: DyT + RoPE; v: copied)
 //     and its 64 queries (q, q_diff: DyT + RoPE + softmax scale), one (row, RoPE group pair) task each, so the
-//     rotation partner and the cos/sin slice are in the thread's own registers.
+//     rotation partner and the cos/sin slice are in the thread's own registers. For bf16 inputs with C <= 1 the
+//     V rows skip the prep waves: the attention waves copy them from HBM straight into a spare V ring slot
+//     (global_load_lds) a step ahead.
 // Two barriers per step: after the first the prep waves store the new tile into the retired slot and the new
 // queries into the query buffer; the second publishes them. The prep waves run at a higher issue priority.
 //
@@ -36,9 +38,12 @@
 //
 // The runs are the flattened (batch, head, step) range split evenly over one workgroup per CU; consecutive
 // workgroups go to different XCDs, so the same run position of every head (the same RoPE rows) shares an L2.
+#include <type_traits>
+
 #include "api.h"
 #include "attn_tile.h"
 #include "common.h"
+#include "tiles.h"
 
 namespace hb {
 namespace band_ring {
@@ -48,7 +53,7 @@ constexpr int NT = 512;       // 8 waves
 constexpr int QT = 64;        // queries per step
 constexpr int KT = 64;        // keys per ring tile
 constexpr int TE = KT * D;    // elements of one tensor in a tile (8 KB)
-constexpr int TILE = 3 * TE;  // K, K_diff, V
+constexpr int KTILE = 2 * TE; // K, K_diff of one ring slot
 constexpr int XF = 2 * 2 * 16 * 64;  // exchange floats: 2 query halves x 2 d-tiles x 16 registers x 64 lanes
 
 // Physical element offset of logical 16-byte chunk c of row r. K, K_diff, q, q_diff: the MFMA operand reads
@@ -70,14 +75,17 @@ struct Prepped {
 struct Par {
   float g1[8], b1[8], g2[8], b2[8];
 };
-__device__ __forceinline__ Par load_par(const float* __restrict__ par, int m1, int m2) {
+// -2 gamma and gamma + beta of groups m1, m2 from `dyt` = [alpha, gamma[D], beta[D]].
+__device__ __forceinline__ Par load_par(const float* __restrict__ dyt, int m1, int m2) {
   Par p;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    p.g1[j] = par[8 * m1 + j];
-    p.b1[j] = par[D + 8 * m1 + j];
-    p.g2[j] = par[8 * m2 + j];
-    p.b2[j] = par[D + 8 * m2 + j];
+    const float ga = dyt[1 + 8 * m1 + j], be = dyt[1 + D + 8 * m1 + j];
+    const float gc = dyt[1 + 8 * m2 + j], bd = dyt[1 + D + 8 * m2 + j];
+    p.g1[j] = -2.f * ga;
+    p.b1[j] = ga + be;
+    p.g2[j] = -2.f * gc;
+    p.b2[j] = gc + bd;
   }
   return p;
 }
@@ -254,13 +262,28 @@ struct Stage {
   u32x4 v[2];
 };
 
+// V rows reach the ring by DMA (global_load_lds, issued by the attention waves a step ahead, into one spare ring
+// slot) for bf16 inputs and windows of at most 64 keys, where the prep waves' row loads set the pace. Half inputs
+// are converted to bf16 on the way, so their V rows pass through the prep waves' registers; at C = 2 the spare
+// slot would fill the LDS, and the copy measured no faster there, so the prep waves load V as well.
+template <class IO, int C>
+constexpr bool kVdma = std::is_same<IO, Bf16Io>::value && C <= 1;
+// V ring slots: one more than the key ring when the next tile's copy lands a step ahead.
+template <class IO, int C>
+constexpr int kVring = 2 * C + 1 + (kVdma<IO, C> ? 1 : 0);
+
+// Ring slot of key tile kt (kt >= -C) in a ring of n slots.
+__device__ __forceinline__ int ring_slot(int kt, int n) { return (kt % n + n) % n; }
+
 // Prep waves (4-7): fill the ring at the start of each run, then prepare step j + 1 during step j from rows
 // loaded during step j - 1. The step loop is unrolled by two over stage buffers A and B, so a buffer is loaded
 // in one step and consumed in the next without being copied (a copy would wait for the loads to land).
 template <class IO, int C, bool ALLROT>
-__device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16_t* qbuf, const float* qpar,
-                                           const float* kpar, float qa2, float ka2, float qscale) {
+__device__ __forceinline__ void prep_waves(const Args& a, uint16_t* kring, uint16_t* vring, uint16_t* qbuf,
+                                           float qa2, float ka2, float qscale) {
   constexpr int RING = 2 * C + 1;
+  constexpr bool VDMA = kVdma<IO, C>;
+  constexpr int VR = kVring<IO, C>;
   const int t = threadIdx.x;
   const int S = a.S, H = a.H, half = a.half;
   const int64_t HD = static_cast<int64_t>(H) * D;
@@ -270,7 +293,7 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
   int m1, m2;
   pair_groups(pp, h8, m1, m2);
   const bool prot = ALLROT || pp < h8;
-  const Par kp = load_par(kpar, m1, m2), qp = load_par(qpar, m1, m2);
+  const Par kp = load_par(a.k_dyt, m1, m2), qp = load_par(a.q_dyt, m1, m2);
   const Range rg(a);
 
   for (int64_t f = rg.beg; f < rg.end;) {
@@ -304,32 +327,36 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
       }
       return r;
     };
-    // Step jj's rows: key tile jj + C and the queries of step jj.
-    auto load_stage = [&](int jj) {
+    // Step jj's rows: key tile jj + C and the queries of step jj; the tile's V rows only when `withv`.
+    auto load_stage = [&](int jj, bool withv) {
       Stage st;
       const int kt = jj + C;
       st.k = load_raw(KT * kt + prow, 1, 4);  // k, k_diff
+      if (withv) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int ch = pt + 256 * u, vpos = KT * kt + (ch >> 3);
-        const int vc = vpos < 0 ? 0 : (vpos < S ? vpos : S - 1);
-        st.v[u] = ld16(xb + static_cast<int64_t>(vc) * a.rs + 2 * HD + 8 * (ch & 7));
+        for (int u = 0; u < 2; ++u) {
+          const int ch = pt + 256 * u, vpos = KT * kt + (ch >> 3);
+          const int vc = vpos < 0 ? 0 : (vpos < S ? vpos : S - 1);
+          st.v[u] = ld16(xb + static_cast<int64_t>(vc) * a.rs + 2 * HD + 8 * (ch & 7));
+        }
       }
       st.q = load_raw(QT * jj + prow, 0, 3);  // q, q_diff
       return st;
     };
-    auto store_tile = [&](int kt, const Prepped& ko, const u32x4 (&v)[2]) {
-      uint16_t* base = ring + ((kt % RING + RING) % RING) * TILE;
+    auto store_k = [&](int kt, const Prepped& ko) {
+      uint16_t* base = kring + ring_slot(kt, RING) * KTILE;
       *reinterpret_cast<u32x4*>(base + kofs(prow, m1)) = ko.a1;
       *reinterpret_cast<u32x4*>(base + kofs(prow, m2)) = ko.a2;
       *reinterpret_cast<u32x4*>(base + TE + kofs(prow, m1)) = ko.b1;
       *reinterpret_cast<u32x4*>(base + TE + kofs(prow, m2)) = ko.b2;
+    };
+    auto store_v = [&](int kt, const u32x4 (&v)[2]) {
+      uint16_t* base = vring + ring_slot(kt, VR) * TE;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int ch = pt + 256 * u, vpos = KT * kt + (ch >> 3);
         const bool in = vpos >= 0 && vpos < S;
-        *reinterpret_cast<u32x4*>(base + 2 * TE + vofs(ch >> 3, ch & 7)) =
-            in ? IO::to_bf16x8(v[u]) : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(base + vofs(ch >> 3, ch & 7)) = in ? IO::to_bf16x8(v[u]) : u32x4{0u, 0u, 0u, 0u};
       }
     };
     auto store_q = [&](const Prepped& qo) {
@@ -343,17 +370,18 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
     Prepped ko, qo;
 #pragma unroll 1
     for (int i = 0; i < RING; ++i) {
-      const Stage st = load_stage(j0 - 2 * C + i);  // key tile j0 - C + i (its query rows are not used)
+      const Stage st = load_stage(j0 - 2 * C + i, true);  // key tile j0 - C + i (its query rows are not used)
       prep_task<IO>(st.k, prot, ka2, kp, 1.f, ko);
-      store_tile(j0 - C + i, ko, st.v);
+      store_k(j0 - C + i, ko);
+      store_v(j0 - C + i, st.v);
       if (i == RING - 1) {
-        const Stage sq = load_stage(j0);
+        const Stage sq = load_stage(j0, false);
         prep_task<IO>(sq.q, prot, qa2, qp, qscale, qo);
         store_q(qo);
       }
     }
     // Loads beyond the run's last step read clamped rows and are never stored.
-    Stage A = load_stage(j0 + 1 < j1 ? j0 + 1 : j0);
+    Stage A = load_stage(j0 + 1 < j1 ? j0 + 1 : j0, !VDMA);
     __syncthreads();
 
     // One step: prepare step jj + 1 from `cur`, load step jj + 2 into `nxt`, then store after the first barrier.
@@ -365,10 +393,11 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
       // the attention waves are still busy, instead of letting the compiler sink it past the barrier.
       asm volatile("" ::"v"(ko.a1), "v"(ko.a2), "v"(ko.b1), "v"(ko.b2), "v"(qo.a1), "v"(qo.a2), "v"(qo.b1),
                    "v"(qo.b2));
-      nxt = load_stage(jj + 2 < j1 ? jj + 2 : jj);
+      nxt = load_stage(jj + 2 < j1 ? jj + 2 : jj, !VDMA);
       __syncthreads();  // the attention waves are done with the oldest tile and the query buffer
       if (next) {
-        store_tile(jj + 1 + C, ko, cur.v);
+        store_k(jj + 1 + C, ko);
+        if constexpr (!VDMA) store_v(jj + 1 + C, cur.v);
         store_q(qo);
       }
       __syncthreads();
@@ -386,8 +415,11 @@ __device__ __forceinline__ void prep_waves(const Args& a, uint16_t* ring, uint16
 
 // Attention waves (0-3), wave = (query half, branch).
 template <class IO, int C, bool FAST>
-__device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16_t* qbuf, float* xbuf, float c) {
+__device__ __forceinline__ void attn_waves(const Args& a, uint16_t* kring, uint16_t* vring, uint16_t* qbuf,
+                                           float* xbuf, float c) {
   constexpr int RING = 2 * C + 1;
+  constexpr bool VDMA = kVdma<IO, C>;
+  constexpr int VR = kVring<IO, C>;
   const int lane = threadIdx.x & 63, wave = wave_id(), lr = lane & 31, lh = lane >> 5;
   const int S = a.S, H = a.H, w = a.w;
   const int64_t HD = static_cast<int64_t>(H) * D;
@@ -414,11 +446,33 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
     const int j1 = static_cast<int>(rg.end - f < a.NS - j0 ? j0 + (rg.end - f) : a.NS);
     const int b = bh / H, h = bh % H;
     const float lamh = a.lam ? a.lam[h] : 1.f;
+    const uint16_t* xb = a.qkv + static_cast<int64_t>(b) * S * a.rs + h * D;
     __syncthreads();  // ring fill
+
+    // V rows of key tile kt copied from qkv straight into their ring slot (the slot of tile kt - RING - 1, which
+    // no wave reads after the previous step); each attention wave copies two 1 KB blocks of 8 rows, lane i the
+    // 16-byte chunk that the swizzled layout puts at byte 16 i of its block. Rows at or past S are zeroed
+    // instead (their probabilities are 0, and 0 * V must stay 0). The copy has the whole step to land; the wave
+    // waits for it before the step's first barrier.
+    auto v_dma = [&](int kt) {
+      const uint16_t* tb = xb + static_cast<int64_t>(KT * kt) * a.rs;
+      uint16_t* vt = vring + ring_slot(kt, VR) * TE;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int blk = 2 * wave + u, r = 8 * blk + (lane >> 3), ch = (lane & 7) ^ ((r & 3) << 1);
+        if (KT * kt + r < S)
+          lds_dma16(tb, static_cast<uint32_t>((r * a.rs + 2 * HD + 8 * ch) * 2), lds_addr(vt + blk * 512));
+        else
+          *reinterpret_cast<u32x4*>(vt + blk * 512 + 8 * lane) = u32x4{0u, 0u, 0u, 0u};
+      }
+    };
 
     // One step of 64 queries. MODE 0: any step; MODE 1 + qh: an interior step of query half qh.
     auto do_step = [&](int j, auto mode) {
       constexpr int MODE = decltype(mode)::value;
+      if constexpr (VDMA) {
+        if (j + 1 < j1) v_dma(j + 1 + C);
+      }
       u32x4 qf[4];
       const uint16_t* qsrc = qbuf + br * TE + 32 * qhalf * D;
 #pragma unroll
@@ -434,11 +488,15 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
       // The wave's tiles form one contiguous range of the ring; the scores of tile i + 1 are issued on the
       // matrix core before the softmax of tile i, so the two overlap.
       const int ilo = (ulo >> 6) - (j - C), ihi = (uhi >> 6) - (j - C);
-      // The wave's tiles span at most RING consecutive slots, starting at the slot of tile ilo.
-      const int kt0 = j - C + ilo, slot0 = (kt0 % RING + RING) % RING;
+      // The wave's tiles span at most RING consecutive slots, starting at the slot of tile ilo (kt0 >= 0).
+      const int kt0 = j - C + ilo, slot0 = kt0 % RING, vslot0 = kt0 % VR;
       auto tile_ptr = [&](int i) {
         const int sl = slot0 + (i - ilo);
-        return ring + (sl >= RING ? sl - RING : sl) * TILE;
+        return kring + (sl >= RING ? sl - RING : sl) * KTILE;
+      };
+      auto vtile_ptr = [&](int i) {
+        const int sl = vslot0 + (i - ilo);
+        return vring + (sl >= VR ? sl - VR : sl) * TE;
       };
       // 32-key half rt of tile i takes part: it meets the band of at least one query of the wave.
       auto active = [&](int i, int rt) {
@@ -458,7 +516,7 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
           act[rt] = active(i, rt);
           full[rt] = k0 >= qa + 31 - w && k1 <= qa + w && k0 >= 0 && k1 <= S - 1;
         }
-        soft_pv<FAST>(sc, tile_ptr(i) + 2 * TE, voff, o, lsum, m, c, act[0], act[1], full[0] ? 0 : 3,
+        soft_pv<FAST>(sc, vtile_ptr(i), voff, o, lsum, m, c, act[0], act[1], full[0] ? 0 : 3,
                       full[1] ? 0 : 3, qlo - kt0 - 4 * lh, static_cast<unsigned>(qhi - qlo));
       };
       // Interior steps (w = 64 C, and every key of the ring tiles j - C .. j + C inside [0, S)): the wave reads
@@ -473,7 +531,7 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
         auto msk = [](int hh) { return (hh == QH ? 1 : 0) | (hh == 4 * C + QH ? 2 : 0); };
         auto fin = [&](int i, const f32x16 (&sc)[2]) {
           const int kt0 = KT * (j - C + i);
-          soft_pv<FAST>(sc, tile_ptr(i) + 2 * TE, voff, o, lsum, m, c, act(2 * i), act(2 * i + 1), msk(2 * i),
+          soft_pv<FAST>(sc, vtile_ptr(i), voff, o, lsum, m, c, act(2 * i), act(2 * i + 1), msk(2 * i),
                         msk(2 * i + 1), qlo - kt0 - 4 * lh, static_cast<unsigned>(qhi - qlo));
           // Each tile's code is scheduled on its own, as in the general loop (measured 2% faster than one
           // schedule over the whole unrolled step).
@@ -533,6 +591,8 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
         for (int jj = 0; jj < 4; ++jj) v[jj] = __fmul_rn(o[1][4 * g + jj], li);
         xs[(give * 4 + g) * 64 + lane] = v;
       }
+      // This step's V copy (and the previous step's output stores) are complete before the barrier.
+      if constexpr (VDMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       {
         const int dt = br;  // the d-tile this wave stores
@@ -585,33 +645,25 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* ring, uint16
 template <class IO, int C>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void band_ring(Args a) {
   constexpr int RING = 2 * C + 1;
-  __shared__ __attribute__((aligned(16))) uint16_t ring[RING * TILE];
+  // K and K_diff of RING tiles; V of RING tiles, plus the spare slot that takes the next tile's copy.
+  __shared__ __attribute__((aligned(16))) uint16_t kring[RING * KTILE];
+  __shared__ __attribute__((aligned(16))) uint16_t vring[kVring<IO, C> * TE];
   __shared__ __attribute__((aligned(16))) uint16_t qbuf[2 * TE];  // q, q_diff of the step (64 rows each)
   __shared__ __attribute__((aligned(16))) float xbuf[XF];
-  __shared__ __attribute__((aligned(16))) float par[4 * D];  // q: -2 gamma, gamma + beta; k: the same
-  const int t = threadIdx.x;
-  if (t < D) {
-    const float qg = a.q_dyt[1 + t], qb = a.q_dyt[1 + D + t], kg = a.k_dyt[1 + t], kb = a.k_dyt[1 + D + t];
-    par[t] = -2.f * qg;
-    par[D + t] = qg + qb;
-    par[2 * D + t] = -2.f * kg;
-    par[3 * D + t] = kg + kb;
-  }
   const SoftmaxPlan plan = softmax_plan(dyt_row_bound<D>(a.q_dyt), dyt_row_bound<D>(a.k_dyt), D);
   const float qa2 = 2.f * kLog2e * a.q_dyt[0], ka2 = 2.f * kLog2e * a.k_dyt[0];
-  __syncthreads();
   if (wave_id() >= 4) {
     // The prep waves issue first when both roles of a SIMD are ready: measured 6% faster than equal priority.
     __builtin_amdgcn_s_setprio(1);
     if (a.half == D / 2)
-      prep_waves<IO, C, true>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
+      prep_waves<IO, C, true>(a, kring, vring, qbuf, qa2, ka2, plan.qscale);
     else
-      prep_waves<IO, C, false>(a, ring, qbuf, par, par + 2 * D, qa2, ka2, plan.qscale);
+      prep_waves<IO, C, false>(a, kring, vring, qbuf, qa2, ka2, plan.qscale);
   }
   else if (plan.fast)
-    attn_waves<IO, C, true>(a, ring, qbuf, xbuf, plan.c);
+    attn_waves<IO, C, true>(a, kring, vring, qbuf, xbuf, plan.c);
   else
-    attn_waves<IO, C, false>(a, ring, qbuf, xbuf, plan.c);
+    attn_waves<IO, C, false>(a, kring, vring, qbuf, xbuf, plan.c);
 }
 
 }  // namespace band_ring
