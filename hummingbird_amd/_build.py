@@ -69,5 +69,51 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+# Host-side sanitizer build (CPU checks of the C ABI's validators): every source's host pass gets AddressSanitizer
+# and UndefinedBehaviorSanitizer; the device code is built as usual. The library is linked without the sanitizer
+# runtime, which the process that loads it preloads (sanitizer_runtime()).
+SAN_DIR = PKG / "_build_san"
+SAN_LIB = SAN_DIR / "libhummingbird_amd.so"
+SANITIZE_HOST_FLAGS = ("-Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefined "
+                       "-Xarch_host -fno-sanitize-recover=undefined -Xarch_host -fno-omit-frame-pointer -Xarch_host -g").split()
+
+
+def sanitizer_runtime() -> Path:
+    """The clang AddressSanitizer runtime (which carries the UndefinedBehaviorSanitizer handlers) of hipcc."""
+    root = Path(hipcc()).resolve().parent.parent / "lib" / "llvm" / "lib" / "clang"
+    if not root.exists():
+        root = Path("/opt/rocm/lib/llvm/lib/clang")
+    found = sorted(root.glob("*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not found:
+        raise RuntimeError(f"no libclang_rt.asan-x86_64.so under {root}")
+    return found[-1]
+
+
+def build_sanitized(verbose: bool = False) -> Path:
+    """Compile every source with the host sanitizers and link `_build_san/libhummingbird_amd.so`."""
+    SAN_DIR.mkdir(exist_ok=True)
+    objs = [SAN_DIR / (Path(s).stem + ".o") for s in SOURCES]
+
+    def comp(src: Path, obj: Path) -> None:
+        cmd = [hipcc(), *COMMON_FLAGS, *SANITIZE_HOST_FLAGS] + (DEVICE_FLAGS if src.suffix == ".hip" else [])
+        cmd += ["-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc (sanitized host) failed on {src.name}:\n" + res.stderr[-4000:])
+
+    with ThreadPoolExecutor(max_workers=len(SOURCES)) as pool:
+        list(pool.map(lambda so: comp(CSRC / so[0], so[1]), zip(SOURCES, objs)))
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(SAN_LIB)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("sanitized link failed:\n" + res.stdout + res.stderr)
+    return SAN_LIB
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--sanitize" in sys.argv:
+        print(build_sanitized(verbose="-v" in sys.argv))
+    else:
+        print(build(verbose="-v" in sys.argv))

@@ -6,10 +6,12 @@ operator raises `RuntimeError` telling the user to build it (`python -m hummingb
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_char_p, c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libhummingbird_amd.so"
+# HUMMINGBIRD_AMD_LIB names another build of the same library (the host-sanitizer build of `_build.py`).
+LIB_PATH = Path(os.environ.get("HUMMINGBIRD_AMD_LIB") or Path(__file__).resolve().parent / "libhummingbird_amd.so")
 
 HB_OK = 0
 HB_BF16 = 0

@@ -61,6 +61,15 @@ int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int 
   if (row_stride < static_cast<int64_t>(5) * H * D || row_stride % 8 != 0)
     return fail(HB_ERR_STRIDE, "row_stride %lld must be >= 5*H*D=%lld and a multiple of 8",
                 static_cast<long long>(row_stride), static_cast<long long>(5) * H * D);
+  return check_extent("attention", "qkv", static_cast<int64_t>(B) * N, row_stride, static_cast<int64_t>(5) * H * D);
+}
+
+int check_extent(const char* what, const char* name, int64_t N, int64_t stride, int64_t C) {
+  constexpr __int128 kLimit = static_cast<__int128>(1) << 48;
+  const __int128 ext = static_cast<__int128>(N > 1 ? N - 1 : 0) * stride + C;
+  if (stride < 0 || C < 0 || ext >= kLimit)
+    return fail(HB_ERR_STRIDE, "%s: %s spans 2^48 elements or more (%lld rows, row stride %lld)", what, name,
+                static_cast<long long>(N), static_cast<long long>(stride));
   return HB_OK;
 }
 

@@ -39,7 +39,11 @@ int check_common(int dtype, int64_t row_stride, int B, int N, int H, int D, int 
 // the conservative test of the two byte extents. NULL never overlaps.
 bool regions_overlap(const void* a, int64_t as, int64_t ca, const void* b, int64_t bs, int64_t cb, int64_t N,
                      int esize);
-// Bytes spanned by N rows of C elements of `esize` bytes, rows `stride` elements apart.
+// Fails with HB_ERR_STRIDE unless N >= 1 rows of C elements, `stride` elements apart, span fewer than 2^48
+// elements (computed without overflow), so that every extent and offset the validators and launchers compute for
+// the buffer fits in int64. Every entry point checks each strided buffer with it before using rows_bytes.
+int check_extent(const char* what, const char* name, int64_t N, int64_t stride, int64_t C);
+// Bytes spanned by N rows of C elements of `esize` bytes, rows `stride` elements apart (after check_extent).
 inline int64_t rows_bytes(int64_t N, int64_t stride, int64_t C, int esize) { return ((N - 1) * stride + C) * esize; }
 // Fails with HB_ERR_STRIDE if the byte ranges [a, a + a_bytes) and [b, b + b_bytes) intersect (NULL never does):
 // an output or workspace of the attention and projection entry points against the buffers the same call reads.

@@ -21,11 +21,12 @@ namespace {
 constexpr int kQdSec = 1;
 constexpr int kKSec = 0, kKdSec = 1, kVSec = 2;
 
-int check_stride(const char* what, int64_t row_stride, int64_t min_elems) {
+// `rows` rows of `min_elems` elements, `row_stride` apart.
+int check_stride(const char* what, int64_t row_stride, int64_t min_elems, int64_t rows) {
   if (row_stride < min_elems || row_stride % 8 != 0)
     return fail(HB_ERR_STRIDE, "%s row_stride %lld must be >= %lld and a multiple of 8", what,
                 static_cast<long long>(row_stride), static_cast<long long>(min_elems));
-  return HB_OK;
+  return check_extent("cross_attention", what, rows, row_stride, min_elems);
 }
 
 int check_shape(int dtype, int B, int L, int Nk, int H, int D, float eps) {
@@ -63,9 +64,9 @@ int hb_cross_validate(int dtype, int64_t q_row_stride, int64_t kv_row_stride, in
   clear_error();
   int st = check_shape(dtype, B, L, Nk, H, D, eps);
   if (st) return st;
-  st = check_stride("q", q_row_stride, static_cast<int64_t>(2) * H * D);
+  st = check_stride("q", q_row_stride, static_cast<int64_t>(2) * H * D, static_cast<int64_t>(B) * L);
   if (st) return st;
-  return check_stride("kv", kv_row_stride, static_cast<int64_t>(3) * H * D);
+  return check_stride("kv", kv_row_stride, static_cast<int64_t>(3) * H * D, static_cast<int64_t>(B) * Nk);
 }
 
 int hb_cross_prep(hipStream_t stream, const void* kv, int dtype, int64_t row_stride, const float* k_weight, int B,
@@ -73,7 +74,7 @@ int hb_cross_prep(hipStream_t stream, const void* kv, int dtype, int64_t row_str
   clear_error();
   int st = check_shape(dtype, B, 1, Nk, H, D, eps);
   if (st) return st;
-  st = check_stride("kv", row_stride, static_cast<int64_t>(3) * H * D);
+  st = check_stride("kv", row_stride, static_cast<int64_t>(3) * H * D, static_cast<int64_t>(B) * Nk);
   if (st) return st;
   if (!kv || !k_weight) return fail(HB_ERR_NULL, "kv and k_weight must be non-NULL");
   if (reinterpret_cast<uintptr_t>(kv) % 16) return fail(HB_ERR_STRIDE, "kv must be 16-byte aligned");
@@ -97,7 +98,7 @@ int hb_cross_attend(hipStream_t stream, const void* q, int dtype, int64_t row_st
   clear_error();
   int st = check_shape(dtype, B, L, Nk, H, D, eps);
   if (st) return st;
-  st = check_stride("q", row_stride, static_cast<int64_t>(2) * H * D);
+  st = check_stride("q", row_stride, static_cast<int64_t>(2) * H * D, static_cast<int64_t>(B) * L);
   if (st) return st;
   if (!q || !q_weight || !k_weight || !out) return fail(HB_ERR_NULL, "q, q_weight, k_weight and out must be non-NULL");
   if (reinterpret_cast<uintptr_t>(q) % 16) return fail(HB_ERR_STRIDE, "q must be 16-byte aligned");

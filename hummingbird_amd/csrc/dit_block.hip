@@ -255,13 +255,30 @@ int check_common(const char* what, int dtype, int64_t N, int C, int L) {
   return HB_OK;
 }
 
+// `rows` rows of `min_stride` elements, `stride` apart.
 int check_tensor(const char* what, const char* name, const void* p, int64_t stride, int64_t min_stride, int dtype,
-                 bool required) {
+                 bool required, int64_t rows) {
   if (!p) return required ? fail(HB_ERR_NULL, "%s: %s must be non-NULL", what, name) : HB_OK;
   if (!aligned16(p)) return fail(HB_ERR_STRIDE, "%s: %s must be 16-byte aligned", what, name);
   if (stride < min_stride || stride % vec_of(dtype))
     return fail(HB_ERR_STRIDE, "%s: %s stride %lld must be >= %lld and a multiple of %d", what, name,
                 static_cast<long long>(stride), static_cast<long long>(min_stride), vec_of(dtype));
+  return check_extent(what, name, rows, stride, min_stride);
+}
+
+// An output region (bytes) against every vector the call reads: a per-channel vector of C elements of `es` bytes
+// (x_bias, local; fp32 weight) or the per-batch rows of the adaLN operands (scale, shift, gate: nb rows `bs`
+// elements apart). Workgroups read these while others write their output rows, so they may share no byte.
+struct Reads {
+  const char* name;
+  const void* p;
+  int64_t bytes;
+};
+int check_out_vs_reads(const char* what, const char* oname, const void* out, int64_t ob, const Reads* r, int n) {
+  for (int i = 0; i < n; ++i) {
+    const int st = check_disjoint(what, oname, out, ob, r[i].name, r[i].p, r[i].bytes);
+    if (st) return st;
+  }
   return HB_OK;
 }
 
@@ -316,20 +333,28 @@ int hb_rms_modulate(hipStream_t stream, const void* x, int dtype, int64_t x_row_
   clear_error();
   int st = check_common("rms_modulate", dtype, N, C, rows_per_batch);
   if (st) return st;
-  if ((st = check_tensor("rms_modulate", "x", x, x_row_stride, C, dtype, true))) return st;
-  if ((st = check_tensor("rms_modulate", "out", out, out_row_stride, C, dtype, true))) return st;
+  if ((st = check_tensor("rms_modulate", "x", x, x_row_stride, C, dtype, true, N))) return st;
+  if ((st = check_tensor("rms_modulate", "out", out, out_row_stride, C, dtype, true, N))) return st;
   if (!weight) return fail(HB_ERR_NULL, "rms_modulate: weight must be non-NULL");
   if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(HB_ERR_EPS, "rms_modulate: eps %g must be finite and >= 0", eps);
   if (!scale != !shift) return fail(HB_ERR_NULL, "rms_modulate: scale and shift are given together or not at all");
   if (scale) {
     if (N % rows_per_batch) return fail(HB_ERR_SHAPE, "rms_modulate: N must be a multiple of rows_per_batch");
     const int64_t stride = N / rows_per_batch > 1 ? mod_batch_stride : C;  // unused with a single batch
-    if ((st = check_tensor("rms_modulate", "scale", scale, stride, C, dtype, true))) return st;
-    if ((st = check_tensor("rms_modulate", "shift", shift, stride, C, dtype, true))) return st;
+    if ((st = check_tensor("rms_modulate", "scale", scale, stride, C, dtype, true, N / rows_per_batch))) return st;
+    if ((st = check_tensor("rms_modulate", "shift", shift, stride, C, dtype, true, N / rows_per_batch))) return st;
   }
   if ((st = check_no_overlap("rms_modulate", "out", out, out_row_stride, C, "x", x, x_row_stride, C, N,
                              dtype == HB_F32 ? 4 : 2, false)))
     return st;
+  {
+    const int es = dtype == HB_F32 ? 4 : 2;
+    const int64_t nb = scale ? N / rows_per_batch : 1, ms = nb > 1 ? mod_batch_stride : C;
+    const Reads r[] = {{"weight", weight, static_cast<int64_t>(C) * 4},
+                       {"scale", scale, rows_bytes(nb, ms, C, es)},
+                       {"shift", shift, rows_bytes(nb, ms, C, es)}};
+    if ((st = check_out_vs_reads("rms_modulate", "out", out, rows_bytes(N, out_row_stride, C, es), r, 3))) return st;
+  }
   if (dtype == HB_BF16)
     launch_rms<uint16_t>(stream, x, x_row_stride, weight, eps, scale, shift, mod_batch_stride, rows_per_batch, out,
                          out_row_stride, N, C);
@@ -349,15 +374,17 @@ int hb_gated_residual(hipStream_t stream, const void* h, int dtype, int64_t h_ro
   clear_error();
   int st = check_common("gated_residual", dtype, N, C, rows_per_batch);
   if (st) return st;
-  if ((st = check_tensor("gated_residual", "h", h, h_row_stride, C, dtype, true))) return st;
-  if ((st = check_tensor("gated_residual", "x", x, x_row_stride, C, dtype, true))) return st;
-  if ((st = check_tensor("gated_residual", "out", out, out_row_stride, C, dtype, true))) return st;
-  if ((st = check_tensor("gated_residual", "x_bias", x_bias, C, C, dtype, false))) return st;
-  if ((st = check_tensor("gated_residual", "local", local, C, C, dtype, false))) return st;
+  if ((st = check_tensor("gated_residual", "h", h, h_row_stride, C, dtype, true, N))) return st;
+  if ((st = check_tensor("gated_residual", "x", x, x_row_stride, C, dtype, true, N))) return st;
+  if ((st = check_tensor("gated_residual", "out", out, out_row_stride, C, dtype, true, N))) return st;
+  if ((st = check_tensor("gated_residual", "x_bias", x_bias, C, C, dtype, false, 1))) return st;
+  if ((st = check_tensor("gated_residual", "local", local, C, C, dtype, false, 1))) return st;
   if (gate) {
     if (N % rows_per_batch) return fail(HB_ERR_SHAPE, "gated_residual: N must be a multiple of rows_per_batch");
     const bool several = N / rows_per_batch > 1;
-    if ((st = check_tensor("gated_residual", "gate", gate, several ? gate_batch_stride : C, C, dtype, true))) return st;
+    if ((st = check_tensor("gated_residual", "gate", gate, several ? gate_batch_stride : C, C, dtype, true,
+                           N / rows_per_batch)))
+      return st;
   }
   if (memory < 0) return fail(HB_ERR_SHAPE, "gated_residual: memory must be >= 0");
   {
@@ -367,6 +394,11 @@ int hb_gated_residual(hipStream_t stream, const void* h, int dtype, int64_t h_ro
         (st = check_no_overlap("gated_residual", "out", out, out_row_stride, C, "x", x, x_row_stride, C, N, es,
                                false)))
       return st;
+    const int64_t nb = gate ? N / rows_per_batch : 1, gs = nb > 1 ? gate_batch_stride : C;
+    const Reads r[] = {{"x_bias", x_bias, static_cast<int64_t>(C) * es},
+                       {"local", local, static_cast<int64_t>(C) * es},
+                       {"gate", gate, rows_bytes(nb, gs, C, es)}};
+    if ((st = check_out_vs_reads("gated_residual", "out", out, rows_bytes(N, out_row_stride, C, es), r, 3))) return st;
   }
   if (dtype == HB_BF16)
     launch_residual<uint16_t>(stream, h, h_row_stride, x, x_row_stride, x_bias, gate, gate_batch_stride, local,
@@ -391,12 +423,12 @@ int hb_residual_rms(hipStream_t stream, const void* h, int dtype, int64_t h_row_
   if (C > 64 * vec_of(dtype) * kResidualRmsChunks)
     return fail(HB_ERR_SHAPE, "residual_rms holds a row in registers: C (%d) must be <= %d", C,
                 64 * vec_of(dtype) * kResidualRmsChunks);
-  if ((st = check_tensor("residual_rms", "h", h, h_row_stride, C, dtype, true))) return st;
-  if ((st = check_tensor("residual_rms", "x", x, x_row_stride, C, dtype, true))) return st;
-  if ((st = check_tensor("residual_rms", "out_h", out_h, out_row_stride, C, dtype, true))) return st;
-  if ((st = check_tensor("residual_rms", "out_y", out_y, out_row_stride, C, dtype, true))) return st;
-  if ((st = check_tensor("residual_rms", "x_bias", x_bias, C, C, dtype, false))) return st;
-  if ((st = check_tensor("residual_rms", "local", local, C, C, dtype, false))) return st;
+  if ((st = check_tensor("residual_rms", "h", h, h_row_stride, C, dtype, true, N))) return st;
+  if ((st = check_tensor("residual_rms", "x", x, x_row_stride, C, dtype, true, N))) return st;
+  if ((st = check_tensor("residual_rms", "out_h", out_h, out_row_stride, C, dtype, true, N))) return st;
+  if ((st = check_tensor("residual_rms", "out_y", out_y, out_row_stride, C, dtype, true, N))) return st;
+  if ((st = check_tensor("residual_rms", "x_bias", x_bias, C, C, dtype, false, 1))) return st;
+  if ((st = check_tensor("residual_rms", "local", local, C, C, dtype, false, 1))) return st;
   if (!weight) return fail(HB_ERR_NULL, "residual_rms: weight must be non-NULL");
   if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(HB_ERR_EPS, "residual_rms: eps %g must be finite and >= 0", eps);
   if (!scale != !shift) return fail(HB_ERR_NULL, "residual_rms: scale and shift are given together or not at all");
@@ -404,10 +436,12 @@ int hb_residual_rms(hipStream_t stream, const void* h, int dtype, int64_t h_row_
   if (gate || scale) {
     if (N % rows_per_batch) return fail(HB_ERR_SHAPE, "residual_rms: N must be a multiple of rows_per_batch");
     const bool several = N / rows_per_batch > 1;
-    if (gate && (st = check_tensor("residual_rms", "gate", gate, several ? gate_batch_stride : C, C, dtype, true)))
+    const int64_t nb = N / rows_per_batch;
+    if (gate && (st = check_tensor("residual_rms", "gate", gate, several ? gate_batch_stride : C, C, dtype, true, nb)))
       return st;
-    if (scale && ((st = check_tensor("residual_rms", "scale", scale, several ? mod_batch_stride : C, C, dtype, true)) ||
-                  (st = check_tensor("residual_rms", "shift", shift, several ? mod_batch_stride : C, C, dtype, true))))
+    if (scale &&
+        ((st = check_tensor("residual_rms", "scale", scale, several ? mod_batch_stride : C, C, dtype, true, nb)) ||
+         (st = check_tensor("residual_rms", "shift", shift, several ? mod_batch_stride : C, C, dtype, true, nb))))
       return st;
   }
   {
@@ -418,6 +452,17 @@ int hb_residual_rms(hipStream_t stream, const void* h, int dtype, int64_t h_row_
         (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "h", h, h_row_stride, C, N, es, false)) ||
         (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "x", x, x_row_stride, C, N, es, false)) ||
         (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "out_h", out_h, out_row_stride, C, N, es, false)))
+      return st;
+    const int64_t nb = (gate || scale) ? N / rows_per_batch : 1;
+    const int64_t gs = nb > 1 ? gate_batch_stride : C, ms = nb > 1 ? mod_batch_stride : C;
+    const Reads r[] = {{"x_bias", x_bias, static_cast<int64_t>(C) * es},
+                       {"local", local, static_cast<int64_t>(C) * es},
+                       {"weight", weight, static_cast<int64_t>(C) * 4},
+                       {"gate", gate, rows_bytes(nb, gs, C, es)},
+                       {"scale", scale, rows_bytes(nb, ms, C, es)},
+                       {"shift", shift, rows_bytes(nb, ms, C, es)}};
+    const int64_t ob = rows_bytes(N, out_row_stride, C, es);
+    if ((st = check_out_vs_reads(w, "out_h", out_h, ob, r, 6)) || (st = check_out_vs_reads(w, "out_y", out_y, ob, r, 6)))
       return st;
   }
   if (dtype == HB_BF16)

@@ -188,7 +188,9 @@ int check_rows(const char* what, int dtype, const void* in, int64_t in_stride, c
   if (!in || !out) return fail(HB_ERR_NULL, "%s input and output must be non-NULL", what);
   if (reinterpret_cast<uintptr_t>(in) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
     return fail(HB_ERR_STRIDE, "%s input and output must be 16-byte aligned", what);
-  return HB_OK;
+  int st = check_extent(what, "input", N, in_stride, in_min);
+  if (st) return st;
+  return check_extent(what, "output", N, out_stride, C);
 }
 
 // Enough 256-thread blocks for every chunk, at most 16 per CU (the rest is walked with the grid stride).
@@ -215,6 +217,9 @@ int hb_dyt(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, c
   if (!dyt) return fail(HB_ERR_NULL, "dyt parameters must be non-NULL");
   const int es = dtype == HB_F32 ? 4 : 2;
   if ((st = check_no_overlap("dyt", "out", out, out_row_stride, C, "x", x, x_row_stride, C, N, es, false))) return st;
+  if ((st = check_disjoint("dyt", "out", out, rows_bytes(N, out_row_stride, C, es), "dyt parameters", dyt,
+                           (1 + 2 * static_cast<int64_t>(C)) * 4)))
+    return st;
   const int chunks = C / (dtype == HB_F32 ? 4 : 8);
   if (dtype == HB_BF16)
     hipLaunchKernelGGL(ew::dyt_kernel<uint16_t>, row_grid(N, chunks), dim3(256), 0, stream,
@@ -238,6 +243,9 @@ int hb_glu(hipStream_t stream, const void* proj, int dtype, int64_t proj_row_str
   // A thread reads the value and gate chunks of its output chunk, which other threads' outputs could cover.
   if ((st = check_no_overlap("glu", "out", out, out_row_stride, F, "proj", proj, proj_row_stride,
                              static_cast<int64_t>(2) * F, N, dtype == HB_F32 ? 4 : 2, false)))
+    return st;
+  if ((st = check_disjoint("glu", "out", out, rows_bytes(N, out_row_stride, F, dtype == HB_F32 ? 4 : 2), "bias", bias,
+                           static_cast<int64_t>(2) * F * 4)))
     return st;
   const int chunks = F / (dtype == HB_F32 ? 4 : 8);
   const dim3 grid = row_grid(N, chunks);
@@ -291,6 +299,14 @@ int hb_residual_dyt(hipStream_t stream, const void* h, int dtype, int64_t h_row_
       (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "x", x, x_row_stride, C, N, es, false)) ||
       (st = check_no_overlap(w, "out_y", out_y, out_row_stride, C, "out_h", out_h, out_row_stride, C, N, es, false)))
     return st;
+  {
+    const int64_t ob = rows_bytes(N, out_row_stride, C, es), cb = static_cast<int64_t>(C) * 4;
+    if ((st = check_disjoint(w, "out_h", out_h, ob, "bias", bias, cb)) ||
+        (st = check_disjoint(w, "out_h", out_h, ob, "dyt parameters", dyt, cb * 2 + 4)) ||
+        (st = check_disjoint(w, "out_y", out_y, ob, "bias", bias, cb)) ||
+        (st = check_disjoint(w, "out_y", out_y, ob, "dyt parameters", dyt, cb * 2 + 4)))
+      return st;
+  }
   const dim3 grid = row_grid(N, C / (dtype == HB_F32 ? 4 : 8));
   if (dtype == HB_BF16)
     hipLaunchKernelGGL(ew::residual_dyt_kernel<uint16_t>, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(h),

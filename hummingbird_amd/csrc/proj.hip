@@ -384,6 +384,7 @@ int check_operand(const char* what, const void* p, int64_t rows, int64_t rs, int
   if (reinterpret_cast<uintptr_t>(p) % 16) return fail(HB_ERR_STRIDE, "%s must be 16-byte aligned", what);
   if (rs < cols || rs % 8) return fail(HB_ERR_STRIDE, "%s row stride %lld must be >= %lld and a multiple of 8", what,
                                        static_cast<long long>(rs), static_cast<long long>(cols));
+  if (const int st = check_extent("projection", what, rows, rs, cols)) return st;
   if (!offsets_fit(rows, rs)) return fail(HB_ERR_SHAPE, "%s spans 4 GiB or more", what);
   return HB_OK;
 }
@@ -479,6 +480,7 @@ extern "C" int hb_proj(hipStream_t stream, const void* x, int dtype, int64_t x_r
   if (!out) return fail(HB_ERR_NULL, "out must be non-NULL");
   if (reinterpret_cast<uintptr_t>(out) % 8 || out_row_stride < F || out_row_stride % 4)
     return fail(HB_ERR_STRIDE, "out must be 8-byte aligned with a row stride >= F and a multiple of 4");
+  if ((st = check_extent("proj", "out", N, out_row_stride, F))) return st;
   {
     const int64_t ob = rows_bytes(N, out_row_stride, F, 2);
     if ((st = check_disjoint("proj", "out", out, ob, "x", x, rows_bytes(N, x_row_stride, K, 2))) ||
@@ -524,6 +526,9 @@ extern "C" int hb_dense_attend_qq(hipStream_t stream, const void* qq, int dtype,
   if (row_stride < static_cast<int64_t>(2) * H * D || row_stride % 8)
     return fail(HB_ERR_STRIDE, "qq row_stride %lld must be >= 2*H*D and a multiple of 8",
                 static_cast<long long>(row_stride));
+  if ((st = check_extent("dense_attend_qq", "qq", static_cast<int64_t>(B) * L, row_stride,
+                         static_cast<int64_t>(2) * H * D)))
+    return st;
   if (half % 8) return fail(HB_ERR_HALF, "half %d must be a multiple of 8", half);
   if (!qq || !q_weight || !k_weight || !out) return fail(HB_ERR_NULL, "qq, q_weight, k_weight and out must be non-NULL");
   if (half > 0 && (!cos || !sin)) return fail(HB_ERR_NULL, "cos and sin must be non-NULL when half > 0");

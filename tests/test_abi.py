@@ -15,6 +15,19 @@ ROOT = Path(__file__).resolve().parents[1]
 HEADER = ROOT / "include" / "hummingbird_amd.h"
 
 
+def _gpu_visible() -> bool:
+    try:
+        import torch
+        return torch.cuda.device_count() > 0  # counts devices without initialising them
+    except Exception:  # noqa: BLE001
+        return False
+
+
+# Tests whose valid-but-fake layouts pass every host check and reach a kernel launch: that launch fails without a
+# GPU, which is what they expect; with a GPU it would run a kernel on fake addresses, so they are CPU-only.
+cpu_only_launch = pytest.mark.skipif(_gpu_visible(), reason="reaches a kernel launch with fake addresses")
+
+
 def declared_functions() -> set[str]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     return set(re.findall(r"\b(hb_[a-z0-9_]+)\s*\(", text))
@@ -263,6 +276,7 @@ def test_row_outputs_that_overlap_their_inputs_are_refused(lib):
 
 
 
+@cpu_only_launch
 def test_row_overlap_check_matches_brute_force(lib):
     """The row-overlap test behind every row-wise entry point, against a byte-by-byte intersection of the rows on
     random layouts (hb_dyt, bf16 rows of 8 elements; fake, never dereferenced addresses). Equal row strides are
@@ -319,3 +333,76 @@ def test_residual_dyt_rejects_before_any_launch(lib):
     assert call(dyt=third, oy=other) == 7                             # out_y aliases x
     assert call(oh=other) == 7                                        # out_h aliases x
     assert call(os=128) == 7                                          # out_h is h with another row stride
+
+
+def test_strides_whose_extent_overflows_are_refused(lib):
+    """A row stride so large that the buffer's rows would span 2^48 elements or more is refused with HB_ERR_STRIDE
+    by every entry point that takes one, before the overlap checks compute any byte extent (which would overflow
+    int64 for such strides; the host-sanitizer build of test_sanitized_host.py traps that arithmetic)."""
+    fake, big = 0x100000, 1 << 61
+    H, D = 4, 64
+    HD = H * D
+    assert dense_validate(lib, row_stride=big) == 7
+    assert "2^48" in lib.hb_last_error().decode()
+    assert lib.hb_band_validate(0, big, 1, 1000, 8, 64, 32, 128) == 7
+    assert lib.hb_cross_validate(0, big, 3 * HD, 2, 100, 257, H, D, 1e-6) == 7
+    assert lib.hb_cross_validate(0, 2 * HD, big, 2, 100, 257, H, D, 1e-6) == 7
+    need = lib.hb_dense_workspace_size(0, 2, 100, H, D)
+    assert lib.hb_dense_diffattn(None, fake, 0, big, fake, fake, fake, fake, 32, None, None, 0x8000000, 2, 100, H, D,
+                                 1e-6, 0x9000000, need) == 7
+    assert lib.hb_band_diffattn(None, fake, 0, big, fake, fake, fake, fake, 32, 16, None, 0x8000000, 1, 100, H, D,
+                                None, 0) == 7
+    assert lib.hb_dense_attend_qq(None, fake, 0, big, fake, fake, fake, fake, 32, None, 0x8000000, 2, 100, H, D, 1e-6,
+                                  0x9000000, need) == 7
+    assert lib.hb_proj(None, fake, 0, big, 0x4000000, 128, 0x8000000, 256, 10, 128, 256) == 7           # x
+    assert lib.hb_proj(None, fake, 0, 128, 0x4000000, 128, 0x8000000, big, 10, 128, 256) == 7           # out
+    assert lib.hb_dit_qkv_proj(None, fake, 0, big, 0x4000000, 256, 256, fake, fake, fake, 32, None, 0x8000000, 2, 100,
+                               H, D, 1e-6, 0x9000000, need) == 7
+    N, C = 20, 64
+    a, b, c = 0x1000000, 0x2000000, 0x3000000
+    assert lib.hb_dyt(None, a, 0, big, c, b, C, N, C) == 7
+    assert lib.hb_dyt(None, a, 0, C, c, b, big, N, C) == 7
+    assert lib.hb_glu(None, a, 0, big, None, 0, b, C, N, C) == 7
+    assert lib.hb_residual_dyt(None, a, 0, C, b, big, None, None, c, None, C, N, C) == 7
+    assert lib.hb_rms_modulate(None, a, 0, big, c, 1e-5, None, None, C, N, b, C, N, C) == 7
+    assert lib.hb_rms_modulate(None, a, 0, C, c, 1e-5, c + 0x10000, c + 0x20000, big, 10, b, C, N, C) == 7  # scale rows
+    assert lib.hb_gated_residual(None, a, 0, C, b, C, None, c, big, None, 0, 10, c + 0x80000, C, N, C) == 7  # gate rows
+    assert lib.hb_residual_rms(None, a, 0, C, b, C, None, None, C, None, 0, c, 1e-5, None, None, C, N,
+                               c + 0x80000, c + 0x90000, big, N, C) == 7
+
+
+@cpu_only_launch
+def test_row_outputs_that_overlap_the_vectors_they_read_are_refused(lib):
+    """The row-wise entry points also refuse an output that shares a byte with the per-batch adaLN rows (scale,
+    shift, gate), the per-channel vectors (bias, local, the fp32 norm weight) or the DyT parameters the same call
+    reads: workgroups read those while others write their rows (HB_ERR_STRIDE; fake, never dereferenced addresses)."""
+    N, C, L = 20, 64, 10                      # bf16 rows of 128 bytes, two batches of 10 rows
+    a, b, out = 0x1000000, 0x2000000, 0x3000000
+    vec = 0x5000000                           # a vector region far from everything
+    ob = ((N - 1) * C + C) * 2                # bytes of the output rows
+    rms = lambda w, scale, shift, o=out: lib.hb_rms_modulate(None, a, 0, C, w, 1e-5, scale, shift, 3 * C, L, o, C,  # noqa: E731
+                                                             N, C)
+    assert rms(vec, vec + 0x1000, vec + 0x2000) in (0, 9)                      # disjoint: reaches the launch
+    assert rms(vec, vec + 0x1000, vec + 0x2000, o=vec + 0x1000 - 128) == 7     # out's last row over scale
+    assert rms(vec, vec + 0x1000, vec + 0x2000, o=vec + 0x2000 + 256) == 7     # out inside shift's second batch row
+    assert rms(out + 64, None, None) == 7                                      # fp32 weight inside out's first row
+    assert "overlaps" in lib.hb_last_error().decode()
+    res = lambda xb, gate, local, o=out: lib.hb_gated_residual(None, a, 0, C, b, C, xb, gate, 2 * C, local, 0, L,  # noqa: E731
+                                                               o, C, N, C)
+    assert res(out + ob - 16, None, None) == 7                                 # x_bias in out's last row
+    assert res(None, out + 128 * 3, None) == 7                                 # gate rows inside out
+    assert res(None, None, out) == 7                                           # local at out's start
+    rr = lambda w, gate, scale, shift, oh, oy: lib.hb_residual_rms(  # noqa: E731
+        None, a, 0, C, b, C, None, gate, 2 * C, None, 0, w, 1e-5, scale, shift, 2 * C, L, oh, oy, C, N, C)
+    assert rr(vec, None, vec + 0x1000, vec + 0x2000, out, out + 0x10000) in (0, 9)  # disjoint: reaches the launch
+    assert rr(vec, None, vec + 0x1000, out + 0x10000 + 512, out, out + 0x10000) == 7  # shift inside out_y
+    assert rr(out + 256, None, None, None, out, out + 0x10000) == 7            # weight inside out_h
+    assert rr(vec, out + ob - 64, None, None, out, out + 0x10000) == 7         # gate over out_h's end
+    dyt_p = lambda o: lib.hb_dyt(None, a, 0, C, vec, o, C, N, C)  # noqa: E731
+    assert dyt_p(vec - 1024) == 7 and dyt_p(vec + 256) == 7                    # out over the DyT parameters
+    glu = lambda bias: lib.hb_glu(None, a, 0, 2 * C, bias, 0, out, C, N, C)  # noqa: E731
+    assert glu(out + 512) == 7                                                 # bias inside out
+    rd = lambda bias, dyt, oy: lib.hb_residual_dyt(None, a, 0, C, b, C, bias, dyt, out, oy, C, N, C)  # noqa: E731
+    assert rd(out + 1024, None, None) == 7                                     # bias inside out_h
+    assert rd(None, vec, vec - 256) == 7                                       # out_y over the DyT parameters
+    assert rd(vec, vec + 0x1000, out + 0x10000) in (0, 9)                      # disjoint: reaches the launch
