@@ -71,9 +71,11 @@ def parse() -> argparse.Namespace:
     return ap.parse_args()
 
 
-def _median_time(fn, target_s: float, min_runs: int = 5) -> tuple[float, int]:
-    """Median wall time (s) of warm runs of `fn`: at least `min_runs`, more until about `target_s` has passed."""
-    fn()  # warm
+def _median_time(fn, target_s: float, min_runs: int = 5, warm: bool = True) -> tuple[float, int]:
+    """Median wall time (s) of runs of `fn` (after one untimed run when `warm`): at least `min_runs`, more until
+    about `target_s` has passed."""
+    if warm:
+        fn()
     times = []
     t_end = time.perf_counter() + target_s
     while len(times) < min_runs or time.perf_counter() < t_end:
@@ -104,9 +106,9 @@ def config0_inputs(seed: int = 0) -> dict:
 
 def cpu_baseline(target_s: float) -> dict:
     """The oracle (NumPy restatement of the reference XLA chains, fp32 with fp32 accumulation, as XLA:CPU runs them)
-    on this host: config 0 whole (to_qkv -> attention -> to_out at L=216), and bounded samples of configs 1 and 2
-    (one of the 48 (batch, head) pairs of a dense call; one of the 8 band heads over 16384 of the 82688 frames),
-    each the median of at least 5 warm runs, scaled to a call and to one clip."""
+    on this host, each workload whole: config 0 (to_qkv -> attention -> to_out at L=216; the median of at least 5
+    warm runs), one config-1 dense call (B=2, L=2584, 24 heads) and one config-2 band call (S=82688, 8 heads,
+    w=128), each the median of 3 runs (multi-second calls: no untimed warm-up run)."""
     from threadpoolctl import threadpool_info
 
     from hummingbird_amd import workloads as wl
@@ -114,7 +116,7 @@ def cpu_baseline(target_s: float) -> dict:
     from oracle import dense as odense
 
     rows = {}
-    # config 0, whole: no sampling
+    # config 0, whole
     c0 = config0_inputs()
 
     def config0():
@@ -126,32 +128,31 @@ def cpu_baseline(target_s: float) -> dict:
     t0, n0 = _median_time(config0, target_s / 3)
     rows["config0"] = {"ms": round(1e3 * t0, 2), "runs": n0, "sampled": "no (whole call, L=216, to_qkv -> "
                        "attention -> to_out)"}
-    # config 1: one full-length (batch, head) pair per run
+    # config 1: one whole dense call
     d, b = wl.DENSE_120S, wl.BAND_120S
-    inp = wl.dense_inputs(1, d["length"], 1, d["head_dim"], seed=0, dtype="fp32")
-    args = (inp["qkv"], inp["q_weight"], inp["k_weight"], inp["inv_freq"], inp["valid"], 1, d["head_dim"], 1e-6,
-            inp["lam"], "fp32", np.float32)
-    t1, n1 = _median_time(lambda: odense.dense_xla(*args), target_s / 3)
-    pairs = d["batch"] * d["heads"]
-    rows["config1_dense_call"] = {"ms": round(1e3 * t1 * pairs, 1), "runs": n1,
-                                  "sampled": f"1 of {pairs} (batch, head) pairs at L={d['length']}, x{pairs}"}
-    # config 2: one head over a 16384-frame slice per run
-    frames = 16384
-    binp = wl.band_inputs(1, frames, 1, b["head_dim"], b["window"], seed=1, dtype="fp32")
-    bargs = (binp["qkv"], binp["q_norm"], binp["k_norm"], binp["inv_freq"], 1, b["head_dim"], b["window"], binp["lam"],
-             "fp32", np.float32)
-    t2, n2 = _median_time(lambda: oband.band_xla(*bargs), target_s / 3)
-    scale = (b["length"] / frames) * b["batch"] * b["heads"]
-    rows["config2_band_call"] = {"ms": round(1e3 * t2 * scale, 1), "runs": n2,
-                                 "sampled": f"1 of {b['heads']} heads over {frames} of {b['length']} frames, "
-                                            f"x{scale:.2f}"}
+    inp = wl.dense_inputs(d["batch"], d["length"], d["heads"], d["head_dim"], seed=0, dtype="fp32")
+    args = (inp["qkv"], inp["q_weight"], inp["k_weight"], inp["inv_freq"], inp["valid"], d["heads"], d["head_dim"],
+            1e-6, inp["lam"], "fp32", np.float32)
+    t1, n1 = _median_time(lambda: odense.dense_xla(*args), 0.0, min_runs=3, warm=False)  # seconds per run
+    rows["config1_dense_call"] = {"ms": round(1e3 * t1, 1), "runs": n1,
+                                  "sampled": f"no (whole call, B={d['batch']}, L={d['length']}, H={d['heads']})"}
+    del inp, args
+    # config 2: one whole band call
+    binp = wl.band_inputs(b["batch"], b["length"], b["heads"], b["head_dim"], b["window"], seed=1, dtype="fp32")
+    bargs = (binp["qkv"], binp["q_norm"], binp["k_norm"], binp["inv_freq"], b["heads"], b["head_dim"], b["window"],
+             binp["lam"], "fp32", np.float32)
+    t2, n2 = _median_time(lambda: oband.band_xla(*bargs), 0.0, min_runs=3, warm=False)
+    rows["config2_band_call"] = {"ms": round(1e3 * t2, 1), "runs": n2,
+                                 "sampled": f"no (whole call, S={b['length']}, H={b['heads']}, w={b['window']})"}
+    del binp, bargs
     threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
     ms_clip = (wl.DENSE_CALLS_PER_CLIP * rows["config1_dense_call"]["ms"]
                + wl.BAND_CALLS_PER_CLIP * rows["config2_band_call"]["ms"])
     return {"value": round(ms_clip, 1), "unit": "ms/120s-clip", "cores": int(threads), "kind": "port",
-            "sample": (f"oracle (NumPy fp32 XLA-chain restatement, not XLA: jax is absent), medians of >= 5 runs; "
-                       f"clip = {wl.DENSE_CALLS_PER_CLIP} config-1 dense calls + {wl.BAND_CALLS_PER_CLIP} config-2 band "
-                       f"calls, each scaled from its sample; host cpus={len(os.sched_getaffinity(0))}"),
+            "sample": (f"oracle (NumPy fp32 XLA-chain restatement, not XLA: jax is absent), whole calls, medians of "
+                       f"3 runs (config 0: >= 5 warm runs); clip = {wl.DENSE_CALLS_PER_CLIP} config-1 dense calls + "
+                       f"{wl.BAND_CALLS_PER_CLIP} config-2 band calls at the measured per-call times; "
+                       f"host cpus={len(os.sched_getaffinity(0))}"),
             "rows": rows}
 
 

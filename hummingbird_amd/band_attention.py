@@ -15,7 +15,11 @@ from hummingbird_amd import _lib, rotary
 from hummingbird_amd.dense_attention import (SUPPORTED_HEAD_DIMS, _f32, _require_gpu, _row_stride, dtype_code,
                                              rope_tables)
 
-__all__ = ["band_attention", "rope_tables", "pack_dyt"]
+__all__ = ["band_attention", "band_workspace", "rope_tables", "pack_dyt"]
+
+# fp32 calls given no workspace allocate one (it lets every key be prepared once) only up to this size; above it they
+# run the kernel that prepares each query block's key window itself, which needs none.
+FP32_WORKSPACE_CAP = 256 << 20
 
 # RoPE tables keyed by the identity of the caller's inv_freq tensor, the length and the device, and checked against
 # the tensor's version (in-place edits bump it), so a decoder's repeated calls with the same buffer reuse one table
@@ -51,6 +55,22 @@ def pack_dyt(norm: dict, head_dim: int, device: torch.device) -> torch.Tensor:
     return torch.cat([alpha, gamma, beta]).contiguous()
 
 
+def _workspace_bytes(dtype: torch.dtype, batch: int, length: int, num_heads: int, head_dim: int, half: int,
+                     window: int) -> int:
+    half = rotary.aligned_half(half) if half % rotary.ALIGN else half
+    return int(_lib.load().hb_band_workspace_size(dtype_code(dtype), batch, length, num_heads, head_dim, half,
+                                                  int(window)))
+
+
+def band_workspace(batch: int, length: int, num_heads: int, head_dim: int, window: int, half: int,
+                   dtype: torch.dtype, device) -> torch.Tensor | None:
+    """A workspace that `band_attention` calls of this shape can share (`workspace=`), or None when they need none:
+    the bf16 shapes outside the streaming kernel require one; fp32 calls use one if given (every key prepared once).
+    The decoder's block loop allocates it once for all its blocks."""
+    need = _workspace_bytes(dtype, batch, length, num_heads, head_dim, half, window)
+    return torch.empty(need, dtype=torch.uint8, device=device) if need else None
+
+
 def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torch.Tensor, num_heads: int,
                    head_dim: int, window: int, *, rows: int = 1024, halo: int = 32, sub: int = 256,
                    stack: bool = True, interpret: bool = False, lam: torch.Tensor | None = None,
@@ -64,8 +84,10 @@ def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torc
     tiling knobs and are accepted and ignored (the reference's `halo >= window` constraint does not apply: the
     HIP kernel takes any window >= 0). `lam` `(H,)` optionally weights the second branch (default 1, the
     reference). `tables` optionally supplies `(cos, sin)` from `rope_tables(S, inv_freq)`. `workspace` optionally
-    supplies the scratch that bf16 shapes outside the streaming kernel (window > 128 or head_dim 128) need:
-    `hb_band_workspace_size` bytes of uint8 on the same device; it is allocated here when absent. Any rotary
+    supplies the scratch that bf16 shapes outside the streaming kernel (window > 128 or head_dim 128) need, and that
+    fp32 calls use to prepare every key once: `hb_band_workspace_size` bytes of uint8 on the same device
+    (`band_workspace`). When absent it is allocated here for those bf16 shapes, and for fp32 only up to
+    `FP32_WORKSPACE_CAP` bytes (larger fp32 calls run without one). Any rotary
     half-width `inv_freq.shape[0]` in `[0, head_dim / 2]` is taken; one that is not a multiple of 8 runs on a copy
     of `qkv` with the q and k dims reordered (`hummingbird_amd.rotary`).
     """
@@ -113,12 +135,13 @@ def band_attention(qkv: torch.Tensor, q_norm: dict, k_norm: dict, inv_freq: torc
     lib = _lib.load()
     need = int(lib.hb_band_workspace_size(code, batch, length, num_heads, head_dim, half, int(window)))
     ws_p, ws_bytes = 0, 0
-    if need:  # shapes outside the streaming kernel prepare their keys into scratch
-        if workspace is None:
+    if need:  # shapes outside the streaming kernel, and fp32, prepare their keys into scratch
+        if workspace is None and not (code == _lib.HB_F32 and need > FP32_WORKSPACE_CAP):
             workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-        elif workspace.numel() * workspace.element_size() < need or workspace.device != dev:
-            raise ValueError(f"workspace must hold {need} bytes on {dev}")
-        ws_p, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        if workspace is not None:
+            if workspace.numel() * workspace.element_size() < need or workspace.device != dev:
+                raise ValueError(f"workspace must hold {need} bytes on {dev}")
+            ws_p, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     stream = torch.cuda.current_stream(dev).cuda_stream
     status = lib.hb_band_diffattn(stream, qkv.data_ptr(), code, rs, qd.data_ptr(), kd.data_ptr(), cos_p, sin_p, half,
                                   int(window), lam_p, out.data_ptr(), batch, length, num_heads, head_dim, ws_p,

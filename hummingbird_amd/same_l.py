@@ -25,18 +25,20 @@ def use_hip(cfg: SameConfig, qkv: torch.Tensor) -> bool:
 
 
 def attention(x: torch.Tensor, block: dict, cfg: SameConfig, lam: torch.Tensor | None = None,
-              dtype: Dtype | None = None) -> torch.Tensor:
+              dtype: Dtype | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """`to_qkv` -> differential band attention at half-width `sub_chunk_size` -> `to_out` (reference:
     same_l._attention, same_l.py:151-169). `block` holds `self_attn.{to_qkv,to_out}.weight`,
     `self_attn.{q_norm,k_norm}` DyT params and `rope_inv_freq`. `dtype` (a preset of hummingbird_amd.dtypes) casts
-    `x` and the projection weights to its compute dtype; without it they are used as given."""
+    `x` and the projection weights to its compute dtype; without it they are used as given. `workspace` (from
+    `band_attention.band_workspace`) is passed to the band kernel."""
     attn = block["self_attn"]
     if dtype is not None:
         x = x.to(dtype.compute)
     qkv = x @ attn["to_qkv"]["weight"].to(x.dtype).t()
     if use_hip(cfg, qkv):
         out = band_attention.band_attention(qkv, attn["q_norm"], attn["k_norm"], block["rope_inv_freq"],
-                                            cfg.num_heads, cfg.dim_heads, cfg.sub_chunk_size, lam=lam)
+                                            cfg.num_heads, cfg.dim_heads, cfg.sub_chunk_size, lam=lam,
+                                            workspace=workspace)
     else:
         out = xla_chain.band_chain(qkv, attn["q_norm"], attn["k_norm"], block["rope_inv_freq"], cfg.num_heads,
                                    cfg.dim_heads, cfg.sub_chunk_size, lam=lam)
@@ -75,11 +77,12 @@ def block(x: torch.Tensor, params: dict, index: int, cfg: SameConfig,
 
 
 def _block_hip(x: torch.Tensor, y: torch.Tensor, params: dict, index: int, cfg: SameConfig,
-               lam: torch.Tensor | None, next_norm: dict | None) -> tuple[torch.Tensor, torch.Tensor | None]:
+               lam: torch.Tensor | None, next_norm: dict | None,
+               workspace: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
     """A block from its input `x` and `y` = DyT(x; pre_norm) cast: `(out, DyT(out; next_norm) or None)`. The residual
     adds run fused with what surrounds them, with the same roundings: the first with the ff_norm DyT that follows it,
     the second with proj_out's bias add before it and, given `next_norm`, the next block's pre_norm DyT after it."""
-    a = attention(y, params, cfg, lam=lam)
+    a = attention(y, params, cfg, lam=lam, workspace=workspace)
     h, y = elementwise.residual_dyt(x, a, norm=params["ff_norm"])
     ff = params["ff"]
     gated = elementwise.glu(y @ ff["glu_proj"]["weight"].t(), cfg.sinusoidal(index), bias=ff["glu_proj"].get("bias"))
@@ -91,13 +94,17 @@ def blocks(x: torch.Tensor, params: list, cfg: SameConfig, lam: torch.Tensor | N
     """The decoder's block loop (reference: same_l.decode, `for index, block in enumerate(params["blocks"])`,
     same_l.py:236-237): `block` over `params` in order. With `attention="hip"` each block hands the next one its
     pre_norm DyT from the pass that finishes its own residual, so a chain of n blocks makes one DyT pass instead of
-    n; the values are those of the block-by-block loop."""
+    n; the values are those of the block-by-block loop. The band kernel's workspace, where the shape takes one
+    (fp32, or bf16 outside the streaming kernel), is allocated once for the whole loop."""
     if not use_hip(cfg, x):
         for index, p in enumerate(params):
             x = block(x, p, index, cfg, lam=lam)
         return x
     y = elementwise.dyt(x, params[0]["pre_norm"])
+    half = params[0]["rope_inv_freq"].shape[0]
+    ws = band_attention.band_workspace(x.shape[0], x.shape[1], cfg.num_heads, cfg.dim_heads, cfg.sub_chunk_size, half,
+                                       x.dtype, x.device)
     for index, p in enumerate(params):
         nxt = params[index + 1]["pre_norm"] if index + 1 < len(params) else None
-        x, y = _block_hip(x, y, p, index, cfg, lam, nxt)
+        x, y = _block_hip(x, y, p, index, cfg, lam, nxt, workspace=ws)
     return x

@@ -112,11 +112,13 @@ def _lam(lam, num_heads: int) -> np.ndarray:
 def dense_xla(qkv: np.ndarray, q_weight: np.ndarray, k_weight: np.ndarray, inv_freq: np.ndarray,
               valid: np.ndarray | None, num_heads: int, head_dim: int, eps: float = 1e-6,
               lam: np.ndarray | None = None, compute: str = "bf16", accum=np.float64,
-              heads_subset: list | None = None) -> np.ndarray:
+              heads_subset: list | None = None, query_rows: np.ndarray | None = None) -> np.ndarray:
     """`(B, L, 5*H*D)` -> `(B, L, H*D)`: the XLA chain of dit._self_attention (dit.py:185-200).
 
     `heads_subset` (a list of (batch, head) pairs) restricts the attention to those heads (the others stay 0);
-    the timed CPU baseline uses it to run a bounded sample of the work.
+    the timed CPU baseline uses it to run a bounded sample of the work. `query_rows` (indices into L) restricts
+    it to those queries against all keys (the other rows stay 0), so long sequences can be checked row by row
+    without the whole `(L, L)` score matrix.
 
     `out = SDPA(q, k, v) - lam * SDPA(q_diff, k_diff, v)` (dit.py:144-146; lam = 1 in the reference), with
     the subtraction's result cast once to the compute dtype. Heads are processed one at a time so the
@@ -126,10 +128,11 @@ def dense_xla(qkv: np.ndarray, q_weight: np.ndarray, k_weight: np.ndarray, inv_f
     b = qkv.shape[0]
     out = np.zeros(q.shape, F32)
     pairs = heads_subset if heads_subset is not None else [(bi, h) for bi in range(b) for h in range(num_heads)]
+    rows = slice(None) if query_rows is None else np.asarray(query_rows)
     for bi, h in pairs:
-        first = sdpa(q[bi, h], k[bi, h], v[bi, h], compute, accum)
-        second = sdpa(qd[bi, h], kd[bi, h], v[bi, h], compute, accum)
-        out[bi, h] = cast(first - lam[h] * second, compute)
+        first = sdpa(q[bi, h][rows], k[bi, h], v[bi, h], compute, accum)
+        second = sdpa(qd[bi, h][rows], kd[bi, h], v[bi, h], compute, accum)
+        out[bi, h][rows] = cast(first - lam[h] * second, compute)
     return merge(out)
 
 

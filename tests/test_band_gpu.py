@@ -146,6 +146,31 @@ def test_band_fp32_without_workspace_vs_oracle(shape):
     assert_fp32_parity(outs[0], outs[1], f"fp32 with vs without workspace {shape}")
 
 
+def test_band_fp32_large_call_allocates_no_workspace(monkeypatch):
+    """An fp32 call whose workspace would exceed band_attention.FP32_WORKSPACE_CAP, given none, runs without one
+    (the kernel that prepares each query block's key window) instead of allocating it; with the cap lowered below
+    a small call's need, the small call's output is the same as with its own workspace (fp32 parity)."""
+    announce("band fp32 workspace cap")
+    b, length, h, d, w, half = 1, 1000, 2, 64, 100, 32
+    inp = workloads.band_inputs(b, length, h, d, w, seed=44, dtype="fp32", half=half)
+    with_ws = run_hip(inp, dtype=torch.float32)
+    allocs = []
+    real_empty = torch.empty
+
+    def spy(*a, **kw):
+        if kw.get("dtype") is torch.uint8:
+            allocs.append(a)
+        return real_empty(*a, **kw)
+
+    monkeypatch.setattr(ba, "FP32_WORKSPACE_CAP", 1024)
+    monkeypatch.setattr(torch, "empty", spy)
+    without = run_hip(inp, dtype=torch.float32)
+    monkeypatch.undo()
+    assert not allocs
+    assert_fp32_parity(without, with_ws, "fp32 above the workspace cap vs with a workspace")
+    assert_fp32_parity(without, oracle(inp, "xla", compute="fp32"), "fp32 above the workspace cap vs oracle")
+
+
 def test_band_fp32_identical_branches_cancel():
     announce("band fp32 identical branches")
     inp = workloads.band_inputs(1, 300, 2, 64, 40, seed=5, dtype="fp32")

@@ -287,3 +287,28 @@ def test_blocks_chain_equals_block_by_block():
     got = chained.float().cpu().numpy()
     scale = max(1.0, float(np.abs(ref).max()))
     assert_bf16_parity(got / scale, ref / scale, f"4 blocks hip vs xla (/{scale:.3g})")
+
+
+def test_blocks_chain_shares_one_band_workspace_fp32(monkeypatch):
+    """In fp32 the band kernel prepares every key once into a workspace; same_l.blocks allocates one for the whole
+    loop and hands the same buffer to every block's band call. The values are the block-by-block loop's (whose
+    calls each allocate their own) bit for bit."""
+    announce("same-l blocks fp32 shared workspace")
+    cfg = SameConfig(channels=64, c_mults=(2,), stride=16, transformer_depth=3, sinusoidal_blocks=1, attention="hip")
+    ps = [to_torch(block_params(128, 2, 384, seed=90 + i), DEV, torch.float32) for i in range(3)]
+    x = dev(RNG.standard_normal((1, 500, 128)), torch.float32)
+    seen = []
+    orig = same_l.band_attention.band_attention
+
+    def spy(*a, **kw):
+        seen.append(kw.get("workspace"))
+        return orig(*a, **kw)
+
+    monkeypatch.setattr(same_l.band_attention, "band_attention", spy)
+    chained = same_l.blocks(x, ps, cfg)
+    monkeypatch.undo()
+    assert len(seen) == 3 and seen[0] is not None and all(w is seen[0] for w in seen)
+    h = x
+    for i, p in enumerate(ps):
+        h = same_l.block(h, p, i, cfg)
+    assert torch.equal(chained, h)

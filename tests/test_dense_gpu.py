@@ -221,6 +221,35 @@ def test_dense_380s_vs_torch_chain():
     got = da.dense_attention(qkv, qw, kw, cos, sin, mask, H, D, 32, 1e-6, lam=lam).float().cpu().numpy()
     ref = xla_chain.dense_chain(qkv, qw, kw, freq, valid, H, D, 1e-6, lam=lam).float().cpu().numpy()
     assert_bf16_parity(got, ref, "380s")
+    # the last head of batch row 0 (700 masked values at its end) against the oracle: its first and last 300
+    # queries, each against all 8180 keys
+    h, hd = H - 1, H * D
+    cols = np.concatenate([np.arange(sec * hd + h * D, sec * hd + (h + 1) * D) for sec in range(5)])
+    host = lambda t: t.float().cpu().numpy()  # noqa: E731
+    rows = np.r_[0:300, L - 300:L]
+    sub = odense.dense_xla(np.ascontiguousarray(host(qkv)[0:1, :, cols]), host(qw), host(kw), workloads.inv_freq(32),
+                           host(valid)[0:1], 1, D, 1e-6, host(lam)[h:h + 1], "bf16", query_rows=rows)
+    assert_bf16_parity(got[0, rows, h * D:(h + 1) * D], sub[0, rows], "380s last head vs oracle")
+
+
+@pytest.mark.parametrize("half", [16, 32])
+def test_rope_tables_at_the_380s_band_length_match_the_oracle(half):
+    """hb_rope_tables at S = 261760 (the 380 s decoder sequence, angles up to 2.6e5 rad) against the oracle's
+    tables: the same fp32 angle, cos / sin evaluated in double and rounded once, so they agree to the last bit
+    except where a double result lies within a rounding error of an fp32 rounding boundary (at most 1 ulp)."""
+    S = 261760
+    announce(f"rope tables S={S} half={half}")
+    freq = workloads.inv_freq(half)
+    cos, sin = da.rope_tables(S, torch.from_numpy(freq).to(DEV))
+    rc, rs = odense.rope_tables(S, freq)
+    for got, ref, name in ((cos, rc[:, :half], "cos"), (sin, rs[:, :half], "sin")):
+        g = got.cpu().numpy().reshape(S, half)
+        assert np.isfinite(g).all()
+        ulps = np.abs(g.view(np.int32).astype(np.int64) - np.ascontiguousarray(ref).view(np.int32).astype(np.int64))
+        exact = (ulps == 0).mean()
+        print(f"  {name}: max {ulps.max()} ulp, {exact:.7f} exact", flush=True)
+        assert ulps.max() <= 1, name
+        assert exact >= 0.99999, name
 
 
 def test_dense_split_entry_points_match_the_fused_call():

@@ -147,6 +147,18 @@ def test_dense_identical_branches_and_linearity():
     np.testing.assert_allclose(f(0.3), 0.7 * f(0.0) + 0.3 * f(1.0), atol=1e-6)
 
 
+def test_dense_query_rows_are_the_full_call_rows():
+    """Restricting the chain to some query rows gives exactly those rows of the full call (each query sees every
+    key either way) and zeros elsewhere."""
+    inp = workloads.dense_inputs(2, 90, 2, 64, seed=9)
+    args = (inp["qkv"], inp["q_weight"], inp["k_weight"], inp["inv_freq"], inp["valid"], 2, 64, 1e-6, inp["lam"])
+    full = odense.dense_xla(*args)
+    rows = np.r_[0:7, 60:90]
+    part = odense.dense_xla(*args, query_rows=rows)
+    np.testing.assert_array_equal(part[:, rows], full[:, rows])
+    assert np.count_nonzero(np.delete(part, rows, axis=1)) == 0
+
+
 def test_dense_profiles_agree_within_contract():
     inp = workloads.dense_inputs(2, 120, 2, 64, seed=8)
     args = (inp["qkv"], inp["q_weight"], inp["k_weight"], inp["inv_freq"], inp["valid"], 2, 64, 1e-6, inp["lam"])

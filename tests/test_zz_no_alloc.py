@@ -77,13 +77,14 @@ def test_noalloc_matches_workspace_entry_point():
 def test_noalloc_rejects_shapes_beyond_the_array():
     lib = _lib.load()
     print("\n[case] noalloc too large", flush=True)
-    c = case(2, 3000, 24, 64, 32, torch.bfloat16, 4)  # 3 * 2 * 24 * 3072 * 64 * 2 B = 56.6 MB fits
+    # every buffer is sized for the rejected shape (L = 6000: 92 MB of qkv), so that a regression of the size
+    # check would show up as a wrong status code rather than as kernels reading past short buffers
+    c = case(2, 6000, 24, 64, 32, torch.bfloat16, 4)
     need = int(lib.hb_dense_workspace_size(0, 2, 6000, 24, 64))
     assert need > lib.hb_dense_noalloc_max_bytes()
-    out = torch.empty((2, 3000, 24 * 64), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((2, 6000, 24 * 64), dtype=torch.bfloat16, device=DEV)
     a = list(args(c, out))
-    a[13] = 6000  # L: the call fails on the size before it reads any pointer
-    assert lib.hb_dense_diffattn_noalloc(*a) == 8  # HB_ERR_WORKSPACE
+    assert lib.hb_dense_diffattn_noalloc(*a) == 8  # HB_ERR_WORKSPACE, before anything is launched
     assert b"no-allocation scratch" in lib.hb_last_error()
     with pytest.raises(ValueError):
         _lib.check(lib.hb_dense_diffattn_noalloc(*a), "noalloc")
