@@ -16,7 +16,8 @@
 // each, waves 2-3 branch 2, and the branch-2 waves hand lam * O2 / l2 to the branch-1 waves through LDS. Keys
 // stream through LDS in 64-key tiles (K, K_diff, V). The dense kernel reads the fp32 workspace written by its
 // prep kernel. The band call prepares every key once into a workspace (band_keys_f32: DyT with the device tanhf,
-// RoPE) and streams the prepared tiles (band_attend_ws_f32); without a workspace it prepares the K / K_diff tiles
+// RoPE) and streams the prepared tiles (band_attend_ws_f32, the next tile fetched into registers while the current
+// one is attended); without a workspace it prepares the K / K_diff tiles
 // of each query block's window itself (band_attend_f32).
 #include "api.h"
 #include "attn_tile.h"
@@ -35,6 +36,32 @@ struct F32Tile {
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+
+// The next 64-key tile of prepared K, K_diff and V (three workspace regions of D-float rows) held in registers:
+// fetched from global memory while the current tile is attended, stored into the LDS tile rows after the
+// barrier that retires it, so the loads' latency is hidden behind the tile's MFMAs.
+template <int D>
+struct TileRegs {
+  f32x4 v[3][D / 16];
+  __device__ __forceinline__ void fetch(const float* const (&src)[3], int k0) {
+#pragma unroll
+    for (int s3 = 0; s3 < 3; ++s3)
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        const int ch = threadIdx.x + 256 * i, row = ch / (D / 4), col = (ch % (D / 4)) * 4;
+        v[s3][i] = ld4(src[s3] + static_cast<int64_t>(k0 + row) * D + col);
+      }
+  }
+  __device__ __forceinline__ void store(float* __restrict__ smem) const {
+#pragma unroll
+    for (int s3 = 0; s3 < 3; ++s3)
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) {
+        const int ch = threadIdx.x + 256 * i, row = ch / (D / 4), col = (ch % (D / 4)) * 4;
+        st4(smem + s3 * F32Tile<D>::TILE + row * F32Tile<D>::KP + col, v[s3][i]);
+      }
+  }
+};
 
 // One 64-key tile for one wave: 32 queries (lane % 32) of one branch. `valid(k)` says whether key k of the tile
 // (0..63) takes part for this lane's query.
@@ -272,6 +299,8 @@ __global__ __launch_bounds__(256) void dense_attend_f32(const float* __restrict_
 
   const float* src[3] = {ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D};
   const int nkt = (Lk + 63) / 64;
+  // Loaded through registers into one LDS stage per tile: a register prefetch of the next tile (TileRegs, as in the
+  // band kernel) measured 1.6 % slower here, where the 48 extra registers leave the waves less room.
   for (int t = 0; t < nkt; ++t) {
     // 3 tensors x 64 rows x D floats; rows past Lk are the zero padding of the workspace (t * 64 + 63 < Lkp)
 #pragma unroll
@@ -459,24 +488,26 @@ __global__ __launch_bounds__(256) void band_attend_ws_f32(const float* __restric
   float lsum = 0.f, m = -INFINITY;
   const float c = kLog2e / sqrtf(static_cast<float>(D));
   const int64_t rowbase = static_cast<int64_t>(bh) * Sp;
-  const float* src[3] = {ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D};
+  const float* const src[3] = {ws + rowbase * D, ws + region + rowbase * D, ws + 2 * region + rowbase * D};
   const int kbeg = (q0 - w > 0 ? q0 - w : 0) / 64 * 64;
   const int kend = q0 + 64 + w < S ? q0 + 64 + w : S;
-  for (int k0 = kbeg; k0 < kend; k0 += 64) {  // k0 + 63 < Sp: Sp is a multiple of 128 and k0 < S
-#pragma unroll
-    for (int s3 = 0; s3 < 3; ++s3)
-#pragma unroll
-      for (int i = 0; i < D / 16; ++i) {
-        const int ch = threadIdx.x + 256 * i, row = ch / (D / 4), col = (ch % (D / 4)) * 4;
-        st4(smem + s3 * T::TILE + row * T::KP + col, ld4(src[s3] + static_cast<int64_t>(k0 + row) * D + col));
-      }
-    __syncthreads();
+  TileRegs<D> nxt;  // every tile's rows k0 .. k0 + 63 lie below Sp: Sp is a multiple of 128 and k0 < S
+  nxt.fetch(src, kbeg);
+  nxt.store(smem);
+  __syncthreads();
+  for (int k0 = kbeg; k0 < kend; k0 += 64) {
+    const bool more = k0 + 64 < kend;
+    if (more) nxt.fetch(src, k0 + 64);
     if (k0 <= qw0 + 31 + w && k0 + 63 >= qw0 - w)
       attend_tile_f32<D>(smem + br * T::TILE, smem + 2 * T::TILE, qreg, o, lsum, m, c, [&](int k) {
         const int kk = k0 + k, dist = kk - q;
         return kk < S && dist <= w && -dist <= w;
       });
     __syncthreads();
+    if (more) {
+      nxt.store(smem);
+      __syncthreads();
+    }
   }
   float* orow = q < S ? out + (static_cast<int64_t>(b) * S + q) * HD + h * D : nullptr;
   store_diff_f32<D>(smem, o, lsum, br, lam ? lam[h] : 1.f, orow);
