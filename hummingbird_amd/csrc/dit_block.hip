@@ -309,14 +309,17 @@ void launch_residual(hipStream_t s, const void* h, int64_t hs, const void* x, in
                      N, C);
 }
 
-constexpr int kResidualRmsChunks = 4;  // chunks of 16 bytes per lane: C <= 2048 (bf16, half) or 1024 (fp32)
+// 16-byte chunks of a row per lane: rows of up to 2048 values (4 chunks of 8 bf16 / half, 8 chunks of 4 fp32).
+template <typename T>
+constexpr int kResidualRmsChunks = sizeof(T) == 4 ? 8 : 4;
+constexpr int kResidualRmsMaxC = 2048;
 
 template <typename T>
 void launch_residual_rms(hipStream_t s, const void* h, int64_t hs, const void* x, int64_t xs, const void* xbias,
                          const void* gate, int64_t gs, const void* local, int memory, const float* w, float eps,
                          const void* scale, const void* shift, int64_t ms, int L, void* out_h, void* out_y, int64_t os,
                          int64_t N, int C) {
-  hipLaunchKernelGGL((blk::residual_rms_kernel<T, kResidualRmsChunks>), dim3(static_cast<unsigned>((N + 3) / 4)),
+  hipLaunchKernelGGL((blk::residual_rms_kernel<T, kResidualRmsChunks<T>>), dim3(static_cast<unsigned>((N + 3) / 4)),
                      dim3(256), 0, s, static_cast<const T*>(h), hs, static_cast<const T*>(x), xs,
                      static_cast<const T*>(xbias), static_cast<const T*>(gate), gs, static_cast<const T*>(local), memory,
                      w, eps, static_cast<const T*>(scale), static_cast<const T*>(shift), ms, L, static_cast<T*>(out_h),
@@ -420,9 +423,8 @@ int hb_residual_rms(hipStream_t stream, const void* h, int dtype, int64_t h_row_
   clear_error();
   int st = check_common("residual_rms", dtype, N, C, rows_per_batch);
   if (st) return st;
-  if (C > 64 * vec_of(dtype) * kResidualRmsChunks)
-    return fail(HB_ERR_SHAPE, "residual_rms holds a row in registers: C (%d) must be <= %d", C,
-                64 * vec_of(dtype) * kResidualRmsChunks);
+  if (C > kResidualRmsMaxC)
+    return fail(HB_ERR_SHAPE, "residual_rms holds a row in registers: C (%d) must be <= %d", C, kResidualRmsMaxC);
   if ((st = check_tensor("residual_rms", "h", h, h_row_stride, C, dtype, true, N))) return st;
   if ((st = check_tensor("residual_rms", "x", x, x_row_stride, C, dtype, true, N))) return st;
   if ((st = check_tensor("residual_rms", "out_h", out_h, out_row_stride, C, dtype, true, N))) return st;

@@ -172,7 +172,7 @@ def residual_rms(h: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: fl
                  local: torch.Tensor | None = None, memory: int = 0, scale: torch.Tensor | None = None,
                  shift: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """`gated_residual(h, x, gate, x_bias, local, memory)` and then `rms_modulate` of its result with `weight`, `eps`,
-    `scale`, `shift`, in one pass per row (`hb_residual_rms`; rows of at most 2048 bf16 / half or 1024 fp32 values):
+    `scale`, `shift`, in one pass per row (`hb_residual_rms`; rows of at most 2048 values):
     returns `(h', norm(h'))`, the same values as the two calls. A DiT block's residuals each feed the next norm
     (sa3jax/dit.py:234-236, 237-247, 249-251 into the next block's 231-233)."""
     _require_gpu(h, "h")
@@ -210,5 +210,4 @@ def residual_rms(h: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: fl
 
 def residual_rms_supported(dtype: torch.dtype, channels: int) -> bool:
     """Whether `residual_rms` takes rows of `channels` values of `dtype` (held in registers)."""
-    per_row = 2048 if dtype in (torch.bfloat16, torch.float16) else 1024
-    return channels <= per_row and channels % (8 if per_row == 2048 else 4) == 0
+    return channels <= 2048 and channels % (8 if dtype in (torch.bfloat16, torch.float16) else 4) == 0

@@ -265,7 +265,7 @@ int hb_gated_residual(hipStream_t stream, const void* h, int dtype, int64_t h_ro
                       const void* local, int memory, int rows_per_batch, void* out, int64_t out_row_stride,
                       int64_t N, int C);
 /*   hb_residual_rms   : hb_gated_residual into out_h, then hb_rms_modulate of out_h into out_y, in one pass that
- *                       holds the row in registers (C <= 2048 for bf16 and half, 1024 for fp32); out_h and out_y
+ *                       holds the row in registers (C <= 2048); out_h and out_y
  *                       share out_row_stride. The block's three residuals each feed a norm (dit.py:234-236,
  *                       237-247, and 249-251 into the next block's 231-233). */
 int hb_residual_rms(hipStream_t stream, const void* h, int dtype, int64_t h_row_stride, const void* x,

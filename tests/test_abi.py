@@ -311,7 +311,7 @@ def test_residual_rms_rejects_before_any_launch(lib):
         None, 0, kw.get("w", fake), 1e-5, kw.get("scale", None), kw.get("shift", None), 384, 10,
         kw.get("oh", fake), fake, kw.get("C", 64), kw.get("N", 20), kw.get("C", 64))
     assert call(C=4096) == 2                  # the row must fit in registers
-    assert call(dtype=1, C=2048) == 2         # fp32 rows up to 1024
+    assert call(dtype=1, C=2304) == 2         # fp32 rows up to 2048 as well
     assert call(w=None) == 1 and call(scale=fake) == 1 and call(oh=None) == 1
     assert call(gate=fake, N=25) == 2         # not a whole number of batches
     assert call(dtype=4) == 3
