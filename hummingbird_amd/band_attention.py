@@ -7,11 +7,10 @@ reference's lane tables (band_attention.py:43-58) with `(length, half)` fp32 tab
 """
 from __future__ import annotations
 
-import weakref
-
 import torch
 
 from hummingbird_amd import _lib, rotary
+from hummingbird_amd._derived import derived
 from hummingbird_amd.dense_attention import (SUPPORTED_HEAD_DIMS, _f32, _require_gpu, _row_stride, dtype_code,
                                              rope_tables)
 
@@ -21,38 +20,31 @@ __all__ = ["band_attention", "band_workspace", "rope_tables", "pack_dyt"]
 # run the kernel that prepares each query block's key window itself, which needs none.
 FP32_WORKSPACE_CAP = 256 << 20
 
-# RoPE tables keyed by the identity of the caller's inv_freq tensor, the length and the device, and checked against
-# the tensor's version (in-place edits bump it), so a decoder's repeated calls with the same buffer reuse one table
-# instead of rebuilding it per call. An entry is dropped when its tensor is garbage-collected (weakref.finalize), so
-# callers that build a fresh inv_freq per call do not pile up tables.
-_TABLE_CACHE: dict = {}
-_TABLE_CACHE_MAX = 64
-
 
 def _cached_tables(inv_freq: torch.Tensor, length: int, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
-    key = (id(inv_freq), length, device)
-    hit = _TABLE_CACHE.get(key)
-    alive = hit is not None and hit[0]() is inv_freq
-    if alive and hit[1] == inv_freq._version:
-        return hit[2], hit[3]
-    cos, sin = rope_tables(length, inv_freq.to(device) if inv_freq.device != device else inv_freq)
-    if not alive:  # first entry for this tensor: drop it when the tensor dies
-        if len(_TABLE_CACHE) >= _TABLE_CACHE_MAX:
-            _TABLE_CACHE.clear()
-        weakref.finalize(inv_freq, _TABLE_CACHE.pop, key, None)
-    _TABLE_CACHE[key] = (weakref.ref(inv_freq), inv_freq._version, cos, sin)
-    return cos, sin
+    """The RoPE tables of `inv_freq` at `length`, built once per live, unedited caller tensor (a decoder's blocks
+    share one inv_freq buffer, so its repeated calls reuse one table instead of rebuilding it per call)."""
+    return derived((inv_freq,), ("rope", length, device),
+                   lambda: rope_tables(length, inv_freq.to(device) if inv_freq.device != device else inv_freq))
 
 
-def pack_dyt(norm: dict, head_dim: int, device: torch.device) -> torch.Tensor:
-    """`{alpha: scalar, gamma: (D,), beta: (D,)}` (the DyT params of sa3jax/same_l.py:58-69) -> the C ABI's
-    `[alpha, gamma[0..D), beta[0..D)]` fp32 vector."""
+def _pack_dyt(norm: dict, head_dim: int, device: torch.device) -> torch.Tensor:
     alpha = torch.as_tensor(norm["alpha"]).to(device=device, dtype=torch.float32).reshape(-1)
     gamma = torch.as_tensor(norm["gamma"]).to(device=device, dtype=torch.float32).reshape(-1)
     beta = torch.as_tensor(norm["beta"]).to(device=device, dtype=torch.float32).reshape(-1)
     if alpha.numel() != 1 or gamma.numel() != head_dim or beta.numel() != head_dim:
         raise ValueError(f"DyT params need a scalar alpha and (head_dim={head_dim},) gamma and beta")
     return torch.cat([alpha, gamma, beta]).contiguous()
+
+
+def pack_dyt(norm: dict, head_dim: int, device: torch.device) -> torch.Tensor:
+    """`{alpha: scalar, gamma: (D,), beta: (D,)}` (the DyT params of sa3jax/same_l.py:58-69) -> the C ABI's
+    `[alpha, gamma[0..D), beta[0..D)]` fp32 vector. When the three are tensors the vector is built once per live,
+    unedited set of them (a decoder passes the same params on every call); a Python-number alpha packs anew."""
+    parts = (norm["alpha"], norm["gamma"], norm["beta"])
+    if not all(isinstance(t, torch.Tensor) for t in parts):
+        return _pack_dyt(norm, head_dim, device)
+    return derived(parts, ("dyt", head_dim, device), lambda: _pack_dyt(norm, head_dim, device))
 
 
 def _workspace_bytes(dtype: torch.dtype, batch: int, length: int, num_heads: int, head_dim: int, half: int,

@@ -27,10 +27,10 @@
 // Two barriers per step: after the first the prep waves store the new tile into the retired slot and the new
 // queries into the query buffer; the second publishes them. The prep waves run at a higher issue priority.
 //
-// Steps away from the sequence ends with w = 64 C (all but a few per run at w = 128) have a fixed tile pattern:
-// every ring tile is read, and only the first and the last active 32-key half are cut by the band, each by one
-// edge. Those steps run a separate, fully unrolled loop with that pattern built in; the general loop covers the
-// rest.
+// Steps away from the sequence ends (all but a few per run) have a tile pattern fixed by w alone: the wave's
+// 32-key halves t = -T .. T around the half that holds its own queries take part (T = floor((w + 31) / 32)), and
+// those with |t| >= M = floor((w + 1) / 32) are cut by one band edge (both when t = 0). Those steps run a separate,
+// fully unrolled loop with their pattern built in (four patterns per C); the general loop covers the rest.
 //
 // Rows are 128 B without padding; 16-byte chunks are XOR-swizzled per row so that the K fragment reads
 // (ds_read_b128, 8 or 16 rows per cycle), the transposing V reads (ds_read_b64_tr_b16, 4 rows x 32 B per 16
@@ -123,12 +123,16 @@ __device__ __forceinline__ void prep_task(const Raw& r, bool rot, float a2, cons
   }
 }
 
-// K fragments of one ring tile for an attention wave (key row 32 rt + lr, dims 16 kk + 8 lh .. +8).
-__device__ __forceinline__ void kload(const uint16_t* __restrict__ sk, const int (&koff)[4], u32x4 (&kf)[2][4]) {
+// K fragments of one ring tile for an attention wave (key row 32 rt + lr, dims 16 kk + 8 lh .. +8), for the
+// 32-key halves that take part (act0, act1: wave-uniform, constants in the unrolled interior loops).
+__device__ __forceinline__ void kload(const uint16_t* __restrict__ sk, const int (&koff)[4], u32x4 (&kf)[2][4],
+                                      bool act0 = true, bool act1 = true) {
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
+  for (int rt = 0; rt < 2; ++rt) {
+    if (!(rt == 0 ? act0 : act1)) continue;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) kf[rt][kk] = lds16(sk + rt * 32 * D + koff[kk]);
+  }
 }
 
 // S^T of one ring tile for an attention wave: 64 keys x its 32 queries, for the 32-key halves that take part
@@ -271,6 +275,14 @@ constexpr bool kVdma = std::is_same<IO, Bf16Io>::value && C <= 1;
 // V ring slots: one more than the key ring when the next tile's copy lands a step ahead.
 template <class IO, int C>
 constexpr int kVring = 2 * C + 1 + (kVdma<IO, C> ? 1 : 0);
+
+// The fixed pattern of an interior step for query half QH (see the file comment): the halves t = -T .. T around
+// ring half QH + 2C take part, and those with |t| >= M are masked by the band edge on their side.
+template <int QH, int T, int M>
+struct Interior {
+  static constexpr int qh = QH, t = T, m = M;
+};
+struct General {};
 
 // Ring slot of key tile kt (kt >= -C) in a ring of n slots.
 __device__ __forceinline__ int ring_slot(int kt, int n) { return (kt % n + n) % n; }
@@ -467,9 +479,9 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* kring, uint1
       }
     };
 
-    // One step of 64 queries. MODE 0: any step; MODE 1 + qh: an interior step of query half qh.
+    // One step of 64 queries: `mode` is General (any step) or the Interior pattern of an interior step.
     auto do_step = [&](int j, auto mode) {
-      constexpr int MODE = decltype(mode)::value;
+      using Mode = decltype(mode);
       if constexpr (VDMA) {
         if (j + 1 < j1) v_dma(j + 1 + C);
       }
@@ -506,7 +518,9 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* kring, uint1
       auto scores = [&](int i, const u32x4 (&kf)[2][4], f32x16 (&sc)[2]) {
         qk(kf, qf, sc, active(i, 0), active(i, 1));
       };
-      auto frags = [&](int i, u32x4 (&kf)[2][4]) { kload(tile_ptr(i) + br * TE, koff, kf); };
+      auto frags = [&](int i, u32x4 (&kf)[2][4], bool act0 = true, bool act1 = true) {
+        kload(tile_ptr(i) + br * TE, koff, kf, act0, act1);
+      };
       auto finish = [&](int i, const f32x16 (&sc)[2]) {
         const int kt0 = KT * (j - C + i);
         bool act[2], full[2];
@@ -519,16 +533,19 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* kring, uint1
         soft_pv<FAST>(sc, vtile_ptr(i), voff, o, lsum, m, c, act[0], act[1], full[0] ? 0 : 3,
                       full[1] ? 0 : 3, qlo - kt0 - 4 * lh, static_cast<unsigned>(qhi - qlo));
       };
-      // Interior steps (w = 64 C, and every key of the ring tiles j - C .. j + C inside [0, S)): the wave reads
-      // all RING tiles, half h = 2 i + rt of them takes part iff qhalf <= h <= 4 C + qhalf, and exactly the first
-      // and the last of those are cut by the band edge. That pattern is known at compile time, so the tile loop
-      // is unrolled with no per-tile scalar work and each half's softmax is the masked or unmasked code only.
-      auto run_interior = [&](auto qh) {
-        constexpr int QH = decltype(qh)::value;
-        auto act = [](int hh) { return hh >= QH && hh <= 4 * C + QH; };
-        // the first half is cut by the lower band edge, the last by the upper one (both edges when C = 0 and
-        // the two are the same half)
-        auto msk = [](int hh) { return (hh == QH ? 1 : 0) | (hh == 4 * C + QH ? 2 : 0); };
+      // Interior steps (every key of the wave's halves inside [0, S), so the band is |k - q| <= w unclipped):
+      // ring half h = 2 i + rt sits t = h - (QH + 2C) halves from the wave's own queries; it takes part iff
+      // |t| <= T, and it is cut by the lower band edge (t < 0), the upper one (t > 0) or both (t = 0) iff
+      // |t| >= M. That pattern is known at compile time, so the tile loop over tiles IL .. IH is unrolled with no
+      // per-tile scalar work, each half's softmax is the masked or unmasked code only, and the fragments of
+      // halves that take no part are not read.
+      auto run_interior = [&](auto pattern) {
+        using P = decltype(pattern);
+        constexpr int QH = P::qh, T = P::t, M = P::m, H0 = QH + 2 * C;
+        constexpr int IL = (H0 - T) / 2, IH = (H0 + T) / 2;
+        static_assert(T >= 0 && M >= 0 && M <= T + 1 && IH < RING, "interior pattern");
+        auto act = [](int hh) { return hh - H0 >= -T && hh - H0 <= T; };
+        auto msk = [](int hh) { return (hh - H0 <= -M ? 1 : 0) | (hh - H0 >= M ? 2 : 0); };
         auto fin = [&](int i, const f32x16 (&sc)[2]) {
           const int kt0 = KT * (j - C + i);
           soft_pv<FAST>(sc, vtile_ptr(i), voff, o, lsum, m, c, act(2 * i), act(2 * i + 1), msk(2 * i),
@@ -539,22 +556,23 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* kring, uint1
         };
         u32x4 ka[2][4], kb[2][4];
         f32x16 sa[2], sb[2];
-        frags(0, ka);
-        if (RING > 1) frags(1, kb);
-        qk(ka, qf, sa, act(0), act(1));
+        auto fr = [&](int i, u32x4 (&kf)[2][4]) { frags(i, kf, act(2 * i), act(2 * i + 1)); };
+        fr(IL, ka);
+        if (IL + 1 <= IH) fr(IL + 1, kb);
+        qk(ka, qf, sa, act(2 * IL), act(2 * IL + 1));
 #pragma unroll
-        for (int i = 0; i < RING; i += 2) {
-          if (i + 2 < RING) frags(i + 2, ka);
-          if (i + 1 < RING) qk(kb, qf, sb, act(2 * i + 2), act(2 * i + 3));
+        for (int i = IL; i <= IH; i += 2) {
+          if (i + 2 <= IH) fr(i + 2, ka);
+          if (i + 1 <= IH) qk(kb, qf, sb, act(2 * i + 2), act(2 * i + 3));
           fin(i, sa);
-          if (i + 1 >= RING) break;
-          if (i + 3 < RING) frags(i + 3, kb);
-          if (i + 2 < RING) qk(ka, qf, sa, act(2 * i + 4), act(2 * i + 5));
+          if (i + 1 > IH) break;
+          if (i + 3 <= IH) fr(i + 3, kb);
+          if (i + 2 <= IH) qk(ka, qf, sa, act(2 * i + 4), act(2 * i + 5));
           fin(i + 1, sb);
         }
       };
-      if constexpr (MODE > 0) {
-        run_interior(std::integral_constant<int, MODE - 1>{});
+      if constexpr (!std::is_same<Mode, General>::value) {
+        run_interior(mode);
       } else {
         // The K fragments are read one tile ahead of their MFMAs. The loop is unrolled over the two score and
         // fragment buffers so that all of them stay in fixed registers.
@@ -616,27 +634,43 @@ __device__ __forceinline__ void attn_waves(const Args& a, uint16_t* kring, uint1
       }
       __syncthreads();
     };
-    // Interior steps [ja, jb): w = 64 C and every key of the ring tiles j - C .. j + C inside [0, S), i.e.
-    // 64 j - w >= 0 and 64 j + 63 + w <= S - 1. Each range is its own loop, so that the unrolled interior code
+    // Interior steps [ja, jb): every query's band inside [0, S), i.e. 64 j - w >= 0 (j >= C, since
+    // 64 C >= w) and 64 j + 63 + w <= S - 1. Each range is its own loop, so that the unrolled interior code
     // shares no control flow with the general path.
     int ja = j0, jb = j0;
-    if (w == KT * C && S - QT - w >= 0) {
+    if (S - QT - w >= 0) {
       ja = j0 > C ? j0 : C;
       jb = (S - QT - w) / QT + 1;
       if (jb > j1) jb = j1;
       if (jb < ja) ja = jb = j0;
     }
 #pragma unroll 1
-    for (int j = j0; j < ja; ++j) do_step(j, std::integral_constant<int, 0>{});
-    if (qhalf == 0) {
+    for (int j = j0; j < ja; ++j) do_step(j, General{});
+    auto interior = [&](auto pattern) {
 #pragma unroll 1
-      for (int j = ja; j < jb; ++j) do_step(j, std::integral_constant<int, 1>{});
-    } else {
+      for (int j = ja; j < jb; ++j) do_step(j, pattern);
+    };
+    // The pattern of w: T = 2C - 1 for w <= 64 C - 32, else 2C; M = T - 1 except for w in {64C - 33, 64C - 32}
+    // (T = M = 2C - 1) and w >= 64 C - 1 (T = M = 2C). C = 0 means w = 0: the diagonal half only, both edges.
+    auto by_pattern = [&](auto qh) {
+      constexpr int QH = decltype(qh)::value;
+      if constexpr (C == 0) {
+        interior(Interior<QH, 0, 0>{});
+      } else {
+        const int tw = (w + 31) / 32, mw = (w + 1) / 32;
+        if (tw == 2 * C)
+          mw == 2 * C ? interior(Interior<QH, 2 * C, 2 * C>{}) : interior(Interior<QH, 2 * C, 2 * C - 1>{});
+        else
+          mw == 2 * C - 1 ? interior(Interior<QH, 2 * C - 1, 2 * C - 1>{})
+                          : interior(Interior<QH, 2 * C - 1, 2 * C - 2>{});
+      }
+    };
+    if (qhalf == 0)
+      by_pattern(std::integral_constant<int, 0>{});
+    else
+      by_pattern(std::integral_constant<int, 1>{});
 #pragma unroll 1
-      for (int j = ja; j < jb; ++j) do_step(j, std::integral_constant<int, 2>{});
-    }
-#pragma unroll 1
-    for (int j = jb; j < j1; ++j) do_step(j, std::integral_constant<int, 0>{});
+    for (int j = jb; j < j1; ++j) do_step(j, General{});
     f += j1 - j0;
   }
 }

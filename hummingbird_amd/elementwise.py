@@ -10,6 +10,7 @@ from __future__ import annotations
 import torch
 
 from hummingbird_amd import _lib
+from hummingbird_amd._derived import f32_vector
 from hummingbird_amd.band_attention import pack_dyt
 from hummingbird_amd.dense_attention import _require_gpu, dtype_code
 
@@ -59,7 +60,7 @@ def glu(proj: torch.Tensor, sinusoidal: bool, bias: torch.Tensor | None = None) 
     rows, stride = _rows(proj, "proj")
     bias_p = 0
     if bias is not None:
-        bias = bias.to(device=proj.device, dtype=torch.float32).contiguous().reshape(-1)
+        bias = f32_vector(bias, proj.device)
         if bias.numel() != width:
             raise ValueError(f"bias must have {width} elements")
         bias_p = bias.data_ptr()
@@ -84,7 +85,7 @@ def residual_dyt(h: torch.Tensor, x: torch.Tensor, bias: torch.Tensor | None = N
     _, xs = _rows(x, "x")
     bias_p = 0
     if bias is not None:
-        bias = bias.to(device=h.device, dtype=torch.float32).contiguous().reshape(-1)
+        bias = f32_vector(bias, h.device)
         if bias.numel() != channels:
             raise ValueError(f"bias must have {channels} elements")
         bias_p = bias.data_ptr()

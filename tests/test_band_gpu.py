@@ -266,6 +266,32 @@ def test_band_multistep_runs_vs_torch_chain(shape):
     check_vs_torch_chain(b, s, h, 64, w, half, gm, f"multistep {shape}")
 
 
+# Windows at the edges of the ring kernel's interior-step patterns. For w in (64 (C - 1), 64 C] an interior
+# step's attention wave attends the 32-key halves t = -T .. T around its own queries, T = floor((w + 31) / 32), and
+# masks those with |t| >= M = floor((w + 1) / 32); the pattern changes at w = 64 C - 33, 64 C - 31 and 64 C - 1.
+PATTERN_WINDOWS = [30, 31, 32, 33, 62, 63, 65, 94, 95, 96, 97, 126, 127]
+
+
+@pytest.mark.parametrize("w", PATTERN_WINDOWS)
+def test_band_interior_pattern_windows_vs_torch_chain(w):
+    """Every interior-step pattern of the ring kernel, on both sides of each change, over multistep runs."""
+    announce(f"band bf16 pattern window {w}")
+    check_vs_torch_chain(1, 6000, 2, 64, w, 32, 1.0, f"pattern w={w}")
+
+
+@pytest.mark.parametrize("w", [17, 40])
+def test_band_interior_patterns_running_max_vs_fused_oracle(w):
+    """Interior patterns with masked halves on the running-max softmax (gamma ~ 8 lifts the logit bound). Over so
+    few keys the outputs reach magnitudes where one bf16 step exceeds the contract's absolute bound, so the
+    contract is applied to the output divided by the reference's largest magnitude."""
+    announce(f"band bf16 pattern window {w} gamma 8")
+    inp = workloads.band_inputs(1, 6000, 2, 64, w, seed=6000 + w, half=32, gamma_mean=8.0)
+    got = run_hip(inp)
+    ref = oracle(inp, "fused")
+    scale = float(np.abs(ref).max())
+    assert_bf16_parity(got / scale, ref / scale, f"pattern w={w} gamma 8 vs fused oracle (scaled by {scale:.3g})")
+
+
 TILED = [  # (B, S, H, D, window, half, gamma_mean): windows past 128 and head_dim 128 (the tiled kernels)
     (1, 5000, 2, 64, 256, 32, 1.0), (2, 3001, 2, 64, 129, 16, 1.0), (1, 4100, 1, 64, 700, 24, 1.0),
     (2, 3000, 2, 128, 128, 64, 1.0), (1, 4000, 2, 128, 300, 48, 1.0), (1, 3000, 2, 128, 17, 0, 1.0),

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from hummingbird_amd import _derived
 from hummingbird_amd import band_attention as ba
 from hummingbird_amd import workloads, xla_chain
 from oracle import band as oband
@@ -78,20 +79,45 @@ def test_band_table_cache_follows_tensor_lifetime(monkeypatch):
         return torch.zeros(length, inv_freq.shape[0]), torch.zeros(length, inv_freq.shape[0])
 
     monkeypatch.setattr(ba, "rope_tables", fake_tables)
-    monkeypatch.setattr(ba, "_TABLE_CACHE", {})
+    monkeypatch.setattr(_derived, "_CACHE", {})
     dev = torch.device("cpu")
     f = torch.ones(4)
     a = ba._cached_tables(f, 10, dev)
     assert ba._cached_tables(f, 10, dev)[0] is a[0] and built == [10]
     f.mul_(2.0)  # an in-place edit bumps the version: rebuilt
     ba._cached_tables(f, 10, dev)
-    assert built == [10, 10] and len(ba._TABLE_CACHE) == 1
+    assert built == [10, 10] and len(_derived._CACHE) == 1
     ba._cached_tables(f, 12, dev)
-    assert len(ba._TABLE_CACHE) == 2
+    assert len(_derived._CACHE) == 2
     for _ in range(5):  # a fresh tensor per call does not pile up entries
         ba._cached_tables(torch.ones(4), 10, dev)
         gc.collect()
-    assert len(ba._TABLE_CACHE) == 2
+    assert len(_derived._CACHE) == 2
     del f, a
     gc.collect()
-    assert len(ba._TABLE_CACHE) == 0
+    assert len(_derived._CACHE) == 0
+
+
+def test_dyt_params_and_bias_vectors_are_converted_once_per_tensor(monkeypatch):
+    """A decoder passes the same DyT params and biases to every call: the packed `[alpha | gamma | beta]` vector and
+    the fp32 bias are built once per live, unedited set of tensors, rebuilt after an in-place edit of any of them,
+    and dropped with them; a Python-number alpha, or an fp32 vector already in place, is used without an entry."""
+    monkeypatch.setattr(_derived, "_CACHE", {})
+    dev = torch.device("cpu")
+    norm = {"alpha": torch.tensor(0.5), "gamma": torch.arange(4.0), "beta": torch.full((4,), 2.0)}
+    p = ba.pack_dyt(norm, 4, dev)
+    assert p.tolist() == [0.5, 0, 1, 2, 3, 2, 2, 2, 2] and ba.pack_dyt(norm, 4, dev) is p
+    norm["beta"].add_(1.0)  # an edit of any one of the three rebuilds the vector
+    q = ba.pack_dyt(norm, 4, dev)
+    assert q is not p and q.tolist()[-1] == 3.0 and len(_derived._CACHE) == 1
+    with pytest.raises(ValueError, match="scalar alpha"):
+        ba.pack_dyt(norm, 3, dev)
+    assert ba.pack_dyt({**norm, "alpha": 0.25}, 4, dev).tolist()[0] == 0.25 and len(_derived._CACHE) == 1
+    b16 = torch.linspace(-1, 1, 6).to(torch.bfloat16)
+    v = _derived.f32_vector(b16, dev)
+    assert v.dtype == torch.float32 and torch.equal(v, b16.float()) and _derived.f32_vector(b16, dev) is v
+    f = torch.ones(3)
+    assert _derived.f32_vector(f, dev).data_ptr() == f.data_ptr() and len(_derived._CACHE) == 2
+    del norm, p, q, b16, v
+    gc.collect()
+    assert len(_derived._CACHE) == 0

@@ -83,7 +83,7 @@ def test_dense_f16_120s_vs_torch_chain():
 
 BAND = [  # (B, S, H, D, window, half): the ring kernel (D = 64, w <= 128) and the tiled pair (w = 256, D = 128)
     (1, 300, 2, 64, 17, 16), (2, 700, 2, 64, 128, 32), (1, 9000, 3, 64, 64, 32), (1, 3000, 2, 64, 256, 32),
-    (1, 2000, 2, 128, 128, 64),
+    (1, 2000, 2, 128, 128, 64), (1, 6000, 2, 64, 40, 32), (1, 6000, 2, 64, 100, 32),
 ]
 
 
