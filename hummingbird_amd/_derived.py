@@ -19,7 +19,10 @@ _CACHE_MAX = 256
 
 
 def derived(sources: tuple[torch.Tensor, ...], key: tuple, make: Callable[[], object]):
-    """`make()`, or the value it returned for the same live, unedited `sources` and the same `key`."""
+    """`make()`, or the value it returned for the same live, unedited `sources` and the same `key`. Tensors made
+    under `torch.inference_mode` keep no version counter, so values derived from them are not kept."""
+    if any(s.is_inference() for s in sources):
+        return make()
     full = (tuple(id(s) for s in sources), key)
     versions = tuple(s._version for s in sources)
     hit = _CACHE.get(full)

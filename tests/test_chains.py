@@ -121,3 +121,8 @@ def test_dyt_params_and_bias_vectors_are_converted_once_per_tensor(monkeypatch):
     del norm, p, q, b16, v
     gc.collect()
     assert len(_derived._CACHE) == 0
+    with torch.inference_mode():  # inference tensors have no version counter: converted per call, nothing kept
+        inf = {"alpha": torch.tensor(0.5), "gamma": torch.ones(4), "beta": torch.zeros(4)}
+        assert ba.pack_dyt(inf, 4, dev).tolist() == [0.5, 1, 1, 1, 1, 0, 0, 0, 0]
+        assert torch.equal(_derived.f32_vector(torch.ones(3, dtype=torch.bfloat16), dev), torch.ones(3))
+    assert len(_derived._CACHE) == 0
