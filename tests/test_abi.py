@@ -8,6 +8,8 @@ import re
 from pathlib import Path
 
 import pytest
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
 
 from hummingbird_amd import _lib
 
@@ -96,6 +98,49 @@ def test_band_validate(lib, kw, status):
     a = {**dict(dtype=0, row_stride=5 * 8 * 64, B=1, S=82688, H=8, D=64, half=32, window=128), **kw}
     assert lib.hb_band_validate(a["dtype"], a["row_stride"], a["B"], a["S"], a["H"], a["D"], a["half"],
                                 a["window"]) == status
+
+
+def _expected_status(dtype, row_stride, B, N, H, D, half, last):
+    """The validators' contract (include/hummingbird_amd.h) restated check by check, in the order the status
+    codes take precedence: dtype, head_dim, shape, half, row stride, extent, then the entry point's own last check
+    (`last`: the status it returns, or 0)."""
+    if dtype not in (0, 1, 2):
+        return 3
+    if D not in (64, 128):
+        return 4
+    if B < 1 or N < 1 or H < 1 or B > 65535 or H > 65535 or N > 1 << 28 or B * N * H * D > 1 << 40:
+        return 2
+    if half < 0 or 2 * half > D:
+        return 5
+    if row_stride < 5 * H * D or row_stride % 8:
+        return 7
+    if (B * N - 1) * row_stride + 5 * H * D >= 1 << 48:
+        return 7
+    return last
+
+
+_EXTREME = st.sampled_from([0, -1, 65535, 65536, 1 << 28, (1 << 28) + 1, (1 << 31) - 1, -(1 << 31)])
+_DIM = st.one_of(st.integers(1, 64), st.integers(1, 64), st.integers(1, 1 << 20), _EXTREME)
+
+
+@settings(max_examples=400, deadline=None, suppress_health_check=[HealthCheck.function_scoped_fixture])
+@given(dtype=st.sampled_from([0, 0, 1, 2, 2, -1, 3]), D=st.sampled_from([64, 64, 128, 128, 96]), B=_DIM, N=_DIM,
+       H=_DIM, half=st.one_of(st.sampled_from([0, 8, 16, 32, 64]), st.integers(-1, 70)),
+       stride_mult=st.one_of(st.integers(1, 4), st.integers(-1, 1 << 24)),
+       stride_pad=st.sampled_from([0, 0, 0, 8, 16, 4, -8]),
+       eps=st.sampled_from([0.0, 1e-6, 1e-6, -1e-6, float("inf"), float("nan")]), window=st.integers(-3, 4096))
+def test_validators_follow_the_contract(lib, dtype, D, B, N, H, half, stride_mult, stride_pad, eps, window):
+    """hb_dense_validate and hb_band_validate against the header's rules on random arguments, including extreme
+    strides and shapes (these paths run only host code)."""
+    h = max(H, 1)
+    row_stride = stride_mult * 5 * h * D + stride_pad
+    if not -(1 << 62) < row_stride < 1 << 62:
+        return
+    eps_ok = eps >= 0.0 and eps != float("inf") and eps == eps
+    assert lib.hb_dense_validate(dtype, row_stride, B, N, H, D, half, eps) == \
+        _expected_status(dtype, row_stride, B, N, H, D, half, 0 if eps_ok else 10)
+    assert lib.hb_band_validate(dtype, row_stride, B, N, H, D, half, window) == \
+        _expected_status(dtype, row_stride, B, N, H, D, half, 0 if window >= 0 else 6)
 
 
 def test_workspace_size(lib):
