@@ -406,6 +406,40 @@ def block_shape(lib, sp, stream, dev, gen) -> dict:
             "block_us_per_call": pb}
 
 
+def stream_of(dev):
+    import torch
+    return torch.cuda.current_stream(dev)
+
+
+def decoder_gemms(x, p, cfg, stream) -> dict:
+    """One decoder block's glu_proj and proj_out at the clip's shape (p50 of interleaved calls, µs): hipBLASLt
+    followed by this package's GLU / residual kernels against the fused GEMMs that do the same work in their
+    epilogues."""
+    from hummingbird_amd import elementwise, projection
+    ff, dim = p["ff"], x.shape[-1]
+    y = x[0]
+    g = projection.glu_linear(y, ff["glu_proj"]["weight"], ff["glu_proj"]["bias"], True)
+    cases = {
+        "glu_proj_torch_then_glu": lambda: elementwise.glu(y @ ff["glu_proj"]["weight"].t(), True,
+                                                           bias=ff["glu_proj"]["bias"]),
+        "glu_proj_fused": lambda: projection.glu_linear(y, ff["glu_proj"]["weight"], ff["glu_proj"]["bias"], True),
+        "proj_out_torch_then_residual_dyt": lambda: elementwise.residual_dyt(
+            y, g @ ff["proj_out"]["weight"].t(), bias=ff["proj_out"]["bias"], norm=p["pre_norm"]),
+        "proj_out_fused": lambda: projection.residual_linear(g, ff["proj_out"]["weight"], ff["proj_out"]["bias"], y,
+                                                             p["pre_norm"]),
+        "to_out_torch_then_residual_dyt": lambda: elementwise.residual_dyt(
+            y, y @ p["self_attn"]["to_out"]["weight"].t(), norm=p["ff_norm"]),
+        "to_out_fused": lambda: projection.residual_linear(y, p["self_attn"]["to_out"]["weight"], None, y,
+                                                           p["ff_norm"]),
+    }
+    rows = {k: [] for k in cases}
+    for _ in range(3):
+        for k, fn in cases.items():
+            rows[k].append(call_percentiles(fn, 10, stream)["p50"])
+    del g
+    return {k: round(float(np.median(v)), 2) for k, v in rows.items()}
+
+
 def decoder_shape(dev, gen) -> dict:
     """The SAME-L decoder's 12 blocks for a 120 s clip at the reference's medium geometry (1358 latents x 17 = 23086
     frames, dim 1536 = 24 heads of 64, ff 4608, half-width 17, the last 8 blocks with the sine gate; random weights,
@@ -449,6 +483,9 @@ def decoder_shape(dev, gen) -> dict:
             h = same_l.block(h, p, i, cfg)
         return h
 
+    def fused_projections():
+        return same_l.blocks(x, params, cfg, projections="hip")
+
     def once(fn) -> float:
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
@@ -456,16 +493,19 @@ def decoder_shape(dev, gen) -> dict:
         b.record()
         torch.cuda.synchronize()
         return a.elapsed_time(b)
-    chained(), one_by_one()
+    chained(), one_by_one(), fused_projections()
     torch.cuda.synchronize()
-    times = {"chained": [], "one_by_one": []}
-    for _ in range(7):  # the two loops interleaved, so that a drift of the clock touches both alike
+    times = {"chained": [], "one_by_one": [], "fused": []}
+    for _ in range(7):  # the loops interleaved, so that a drift of the clock touches them alike
         times["chained"].append(once(chained))
         times["one_by_one"].append(once(one_by_one))
+        times["fused"].append(once(fused_projections))
     res = {"shape": {"S": S, "dim": dim, "heads": cfg.num_heads, "ff": ff, "w": cfg.sub_chunk_size,
                      "blocks": cfg.transformer_depth, "sine_blocks": cfg.sinusoidal_blocks},
            "chained_ms_per_clip": round(float(np.median(times["chained"])), 3),
            "block_by_block_ms_per_clip": round(float(np.median(times["one_by_one"])), 3),
+           "hip_projections_ms_per_clip": round(float(np.median(times["fused"])), 3),
+           "projection_gemms_us": decoder_gemms(x, params[0], cfg, stream_of(dev)),
            "reference_whole_decode_ms_tpu_v6e": 61.0}
     del params
     return res

@@ -48,6 +48,10 @@ SIGNATURES = {
                                    c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t]),
     "hb_proj": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int,
                         c_int]),
+    "hb_proj_glu": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_int, c_void_p,
+                            c_int64, c_int64, c_int, c_int]),
+    "hb_proj_residual": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
+                                 c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int]),
     "hb_band_validate": (c_int, [c_int, c_int64, c_int, c_int, c_int, c_int, c_int, c_int]),
     "hb_band_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int, c_int]),
     "hb_band_diffattn": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,

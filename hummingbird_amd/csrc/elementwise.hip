@@ -11,6 +11,7 @@
 // the SiLU; the product); fp32 runs do not round.
 #include "api.h"
 #include "common.h"
+#include "glu_act.h"
 
 namespace hb {
 namespace ew {
@@ -20,7 +21,7 @@ struct Vec;
 template <>
 struct Vec<uint16_t> {  // bf16: 8 elements per 16 bytes
   static constexpr int N = 8;
-  static constexpr bool kHwSine = true;
+  static constexpr int kSine = kSineBf16;
   __device__ static void load(const uint16_t* p, float (&x)[8]) { unpack8(ld16(p), x); }
   __device__ static void store(uint16_t* p, const float (&x)[8]) { st16(p, pack8(x)); }
   __device__ static float round(float x) { return round_bf16(x); }
@@ -28,7 +29,7 @@ struct Vec<uint16_t> {  // bf16: 8 elements per 16 bytes
 template <>
 struct Vec<_Float16> {  // IEEE half (the fp16 preset): 8 elements per 16 bytes
   static constexpr int N = 8;
-  static constexpr bool kHwSine = false;  // half's 11 bits need the library sine near the zeros of sin(pi g)
+  static constexpr int kSine = kSineHalf;
   __device__ static void load(const _Float16* p, float (&x)[8]) { F16Io::unpack8(ld16(p), x); }
   __device__ static void store(_Float16* p, const float (&x)[8]) {
     u32x4 v;
@@ -41,7 +42,7 @@ struct Vec<_Float16> {  // IEEE half (the fp16 preset): 8 elements per 16 bytes
 template <>
 struct Vec<float> {  // fp32: 4 elements per 16 bytes
   static constexpr int N = 4;
-  static constexpr bool kHwSine = false;
+  static constexpr int kSine = kSineLibrary;
   __device__ static void load(const float* p, float (&x)[4]) {
     const f32x4 v = *reinterpret_cast<const f32x4*>(p);
     for (int i = 0; i < 4; ++i) x[i] = v[i];
@@ -75,9 +76,7 @@ __global__ __launch_bounds__(256) void dyt_kernel(const T* __restrict__ x, int64
   }
 }
 
-// The activation with the XLA chain's intermediate arrays: SiLU(g) = g * sigmoid(g) (jax.nn.silu), the sigmoid
-// held in the compute dtype before the product; sin(pi * g) with pi taken in the compute dtype (a Python float
-// times a bf16 array is a bf16 multiply in JAX) and the product held in it before the sine.
+// The activation with the XLA chain's intermediate arrays (glu_act.h), rounded before the product.
 // `bias` (2F values of the compute dtype, or null): the glu_proj layer's bias, added to the GEMM output in the
 // compute dtype first (same_l._linear: the matmul, then the bias add, each held in the compute dtype).
 template <typename T, bool SINE>
@@ -102,27 +101,7 @@ __global__ __launch_bounds__(256) void glu_kernel(const T* __restrict__ proj, in
     }
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-      float act;
-      if constexpr (SINE) {
-        const float t = Vec<T>::round(Vec<T>::round(static_cast<float>(M_PI)) * g[i]);
-        if constexpr (Vec<T>::kHwSine) {
-          // bf16: Cody-Waite reduction of t by 2 pi = C1 + C2 (C1 = 6.28125 has 8 significant bits, so k * C1 is
-          // exact for |k| < 2^16), then the hardware sine (v_sin_f32, argument in revolutions) of the remainder,
-          // |rev| <= 1/2. Its error is far inside the bf16 rounding of the result. Larger |t| take the library sine.
-          constexpr float inv2pi = static_cast<float>(0.5 / M_PI);
-          if (__builtin_expect(fabsf(t) > 65536.f, 0)) {
-            act = sinf(t);
-          } else {
-            const float k = rintf(t * inv2pi);
-            const float r = __fmaf_rn(-k, 1.9353071795864769e-3f, __fmaf_rn(-k, 6.28125f, t));
-            act = __builtin_amdgcn_sinf(r * inv2pi);
-          }
-        } else {
-          act = sinf(t);
-        }
-      } else {
-        act = g[i] * Vec<T>::round(__builtin_amdgcn_rcpf(1.f + fast_exp2(-kLog2e * g[i])));
-      }
+      const float act = glu_act<SINE, Vec<T>::kSine>(g[i], [](float x) { return Vec<T>::round(x); });
       val[i] = val[i] * Vec<T>::round(act);
     }
     Vec<T>::store(out + n * os + c0, val);

@@ -26,8 +26,11 @@
 // four waves computes one head (64 features) for all 128 tokens: 8 MFMAs per 16 columns from 2 + 4 fragment reads.
 #include <math.h>
 
+#include <type_traits>
+
 #include "api.h"
 #include "common.h"
+#include "glu_act.h"
 #include "tiles.h"
 
 namespace hb {
@@ -52,7 +55,7 @@ struct Cfg {
   static_assert(TW >= 1, "at least one token tile per wave");
 };
 
-enum Epilogue { kQkvPrep = 0, kPlain = 1 };
+enum Epilogue { kQkvPrep = 0, kPlain = 1, kResidual = 2 };
 
 // Tokens are tiled over the padded token space: B batches of Lp rows (Lp a multiple of 128), token p of it being row
 // p % Lp of batch p / Lp; rows at or past L of a batch, and past the last batch, are padding.
@@ -74,9 +77,15 @@ struct Args {
   uint16_t* qq;       // (B, L, 2 H 64): [q | q_diff]
   uint16_t* ws;       // workspace: k', k_diff', v'^T regions of `region` elements
   int64_t region;
-  // kPlain
-  uint16_t* out;      // (tokens, F) row-major, row stride out_rs
+  // kPlain, kResidual
+  uint16_t* out;      // (tokens, F) row-major, row stride out_rs (kResidual: out_h)
   int64_t out_rs;
+  // kResidual
+  const uint16_t* res;  // (tokens, F) residual rows, row stride res_rs (may be `out` itself)
+  int64_t res_rs;
+  const float* bias;    // F values of the compute dtype, or null
+  const float* dyt;     // [alpha, gamma[F], beta[F]], or null
+  uint16_t* out_y;      // (tokens, F), row stride out_rs, when dyt is given
 };
 
 // The workgroup's tile: groups of four feature tiles walk the token tiles together (consecutive workgroups share
@@ -303,6 +312,59 @@ __device__ __forceinline__ void epilogue_plain(const Args& a, const f32x16 (&acc
   }
 }
 
+// The residual add of same_l._block (sa3jax/same_l.py:191-192) after the projection (same_l._linear: the matmul,
+// then the bias add): out_h = h + (x W^T + bias), each of the three held in the compute dtype, and with `dyt`
+// out_y = cast(DyT(out_h)), the input of the next GEMM; the same arithmetic as hb_residual_dyt on the stored product.
+// Each element of the residual is read and its out_h written by one lane, so out_h may be the residual itself.
+template <class IO, int NW, int TT>
+__device__ __forceinline__ void epilogue_residual(const Args& a, const f32x16 (&acc)[2][Cfg<NW, TT>::TW], int ft,
+                                                  int p0) {
+  constexpr int TW = Cfg<NW, TT>::TW;
+  const int lane = threadIdx.x & 63, lh = lane >> 5, wv = wave_id();
+  const int fb = ft * FT + 64 * (wv & 3);
+  const float a2 = a.dyt ? 2.f * kLog2e * a.dyt[0] : 0.f;
+  p0 += 32 * TW * (wv >> 2);
+#pragma unroll
+  for (int t = 0; t < TW; ++t) {
+    int b, tok;
+    token_of(a, p0 + 32 * t, b, tok);
+    if (b < 0 || tok >= a.L) continue;
+    float x[8][4];
+    token_values<IO, TW>(acc, t, x);
+    const uint16_t* hrow = a.res + static_cast<int64_t>(tok) * a.res_rs + fb;
+    uint16_t* orow = a.out + static_cast<int64_t>(tok) * a.out_rs + fb;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const int f0 = 8 * g + 4 * lh;  // this lane's four features of group g, relative to fb
+      const u32x2 hp = *reinterpret_cast<const u32x2*>(hrow + f0);
+      float hv[4];
+      {
+        float e8[8];
+        IO::unpack8(u32x4{hp[0], hp[1], 0u, 0u}, e8);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hv[j] = e8[j];
+      }
+      float v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float xv = x[g][j];
+        if (a.bias) xv = IO::round(xv + a.bias[fb + f0 + j]);
+        v[j] = IO::round(hv[j] + xv);
+      }
+      *reinterpret_cast<u32x2*>(orow + f0) = pack4_io<IO>(v);
+      if (a.dyt) {
+        float y[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float gm = a.dyt[1 + fb + f0 + j], be = a.dyt[1 + a.F + fb + f0 + j];
+          y[j] = dyt_tanh(v[j], a2, -2.f * gm, gm + be);
+        }
+        *reinterpret_cast<u32x2*>(a.out_y + static_cast<int64_t>(tok) * a.out_rs + fb + f0) = pack4_io<IO>(y);
+      }
+    }
+  }
+}
+
 // Waits until at most N vector-memory operations of this wave are outstanding (vmcnt N; expcnt and lgkmcnt at their
 // maxima, i.e. not waited on). Loads complete in issue order, so this retires all but the N most recent copies.
 template <int N>
@@ -356,11 +418,156 @@ __global__ __launch_bounds__(64 * NW) void proj_gemm(Args a) {
 
   if constexpr (EPI == kQkvPrep)
     epilogue_qkv<IO, NW, TT>(a, acc, ft, p0);
+  else if constexpr (EPI == kResidual)
+    epilogue_residual<IO, NW, TT>(a, acc, ft, p0);
   else
     epilogue_plain<IO, NW, TT>(a, acc, ft, p0);
 }
 
 }  // namespace proj
+
+// The feed-forward's glu_proj with the GLU in its epilogue (sa3jax/same_l.py:181-183): out = value * act(gate) for
+// [value | gate] = x [W_value | W_gate]^T (+ bias), so the 2F-wide product is never stored.
+//
+// Workgroup tiles of 256 W rows x 256 tokens, four waves of 128 x 128 (4 x 4 tiles of v_mfma_f32_32x32x16, the 256
+// accumulators in the accumulation registers, one wave per SIMD), K in 64-column steps through two 64 KB LDS
+// stages filled by global_load_lds (next step's copy issued at the start of the current one). The 256 W rows of a
+// tile are gathered so that each wave holds the value rows of 64 output features in its MFMA tiles 0 and 1 and the
+// gate rows of the same features in tiles 2 and 3: a lane then has the value and the gate of each of its outputs in
+// the same register of two tiles, and the epilogue needs no exchange. A tile writes 128 output features.
+namespace proj_wide {
+
+constexpr int KS = 64;                 // reduction columns per step
+constexpr int TROWS = 256;             // W rows and tokens per tile
+constexpr int STAGE = 2 * TROWS * KS;  // elements per LDS stage: W rows, then token rows (64 KB)
+
+struct Args {
+  const uint16_t* w;  // (2F, K): value rows 0 .. F - 1, gate rows F .. 2F - 1
+  const uint16_t* x;  // (N, K) token rows
+  int64_t w_rs, x_rs;
+  int K, N, F;        // F: output features (value width)
+  int nF, nT;         // feature tiles (F / 128), token tiles
+  const float* bias;  // 2F values of the compute dtype, or null
+  uint16_t* out;      // (N, F)
+  int64_t out_rs;
+};
+
+// W row of tile row r of feature tile ft: wave half wm = r / 128 covers output features 128 ft + 64 wm .. + 64, its
+// MFMA tile i = (r / 32) % 4 holds value rows (i = 0, 1) or the gate rows of the same features (i = 2, 3).
+__device__ __forceinline__ int w_row(const Args& a, int ft, int r) {
+  const int wm = r >> 7, i = (r >> 5) & 3;
+  const int f = 128 * ft + 64 * wm + 32 * (i & 1) + (r & 31);
+  return i < 2 ? f : a.F + f;
+}
+
+template <class IO, bool SINE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void proj_glu(Args a) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+  int ft, tt;
+  {  // groups of four feature tiles walk the token tiles together; the XCD remap keeps consecutive tiles on one XCD
+    constexpr int GF = 4;
+    const int id = xcd_remap(blockIdx.x, a.nF * a.nT);
+    const int g = id / (GF * a.nT), first = g * GF;
+    const int gsize = a.nF - first < GF ? a.nF - first : GF;
+    const int in = id - g * GF * a.nT;
+    ft = first + in % gsize;
+    tt = in / gsize;
+  }
+  const int lane = threadIdx.x & 63, wv = wave_id(), wm = wv >> 1, wn = wv & 1;
+  const int lr = lane & 31, lh = lane >> 5;
+
+  // Copies: wave wv fills 1 KB blocks wv + 4 u (u < 8) of each operand, block b holding tile rows 8 b .. 8 b + 7;
+  // lane i lands at row 8 b + i / 8, physical chunk i % 8, so it fetches the logical chunk that swz<64> puts there.
+  uint32_t aoff[8], boff[8];
+  {
+    const int r8 = lane >> 3, c = (lane & 7) ^ r8 ^ (wv & 1);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int row = 8 * (wv + 4 * u) + r8;
+      aoff[u] = static_cast<uint32_t>(static_cast<int64_t>(w_row(a, ft, row)) * a.w_rs * 2 + 16 * c);
+      int tok = tt * TROWS + row;
+      if (tok >= a.N) tok = a.N - 1;  // padding rows read a real row; their results are not stored
+      boff[u] = static_cast<uint32_t>(static_cast<int64_t>(tok) * a.x_rs * 2 + 16 * c);
+    }
+  }
+  const uint32_t lds0 = lds_addr(smem);
+  auto copy = [&](int k, int s) {
+    const uint32_t st = lds0 + s * STAGE * 2;
+    const uint16_t* wk = a.w + static_cast<int64_t>(k) * KS;
+    const uint16_t* xk = a.x + static_cast<int64_t>(k) * KS;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      lds_dma16(wk, aoff[u], st + (wv + 4 * u) * 1024);
+      lds_dma16(xk, boff[u], st + TROWS * KS * 2 + (wv + 4 * u) * 1024);
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  // Fragments of 16-column sub-step kk, double-buffered in registers (sub-step kk + 1 is read during kk's MFMAs).
+  u32x4 fa[2][4], fb[2][4];
+  auto fread = [&](const uint16_t* st, int kk, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[buf][i] = lds16(st + swz<64>(128 * wm + 32 * i + lr, 2 * kk + lh));
+      fb[buf][i] = lds16(st + TROWS * KS + swz<64>(128 * wn + 32 * i + lr, 2 * kk + lh));
+    }
+  };
+
+  const int nk = a.K / KS;
+  copy(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int k = 0; k < nk; ++k) {
+    const uint16_t* st = smem + (k & 1) * STAGE;
+    fread(st, 0, 0);
+    if (k + 1 < nk) copy(k + 1, (k + 1) & 1);  // into the stage step k - 1 used (every wave is past its barrier)
+#pragma unroll
+    for (int kk = 0; kk < KS / 16; ++kk) {
+      if (kk + 1 < KS / 16) fread(st, kk + 1, (kk + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_io_32x32x16<IO>(fa[kk & 1][i], fb[kk & 1][j], acc[i][j]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // step k + 1 has landed
+    __syncthreads();
+  }
+
+  // Epilogue: lane lr of token tile j holds, in register 4 q + e of MFMA tile i, feature 8 q + 4 lh + e of that
+  // tile. Value (tiles 0, 1) and gate (tiles 2, 3) are rounded to the compute dtype (the reference's stored
+  // glu_proj output), the bias added and rounded, then value * round(act(gate)) as hb_glu computes it.
+  auto round = [](float v) { return IO::round(v); };
+  constexpr int kSine = std::is_same<IO, Bf16Io>::value ? kSineBf16 : kSineHalf;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tok = tt * TROWS + 128 * wn + 32 * j + lr;
+    if (tok >= a.N) continue;
+    uint16_t* orow = a.out + static_cast<int64_t>(tok) * a.out_rs;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int f = 128 * ft + 64 * wm + 32 * i + 8 * q + 4 * lh;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float val = IO::round(acc[i][j][4 * q + e]), g = IO::round(acc[i + 2][j][4 * q + e]);
+          if (a.bias) {
+            val = IO::round(val + a.bias[f + e]);
+            g = IO::round(g + a.bias[a.F + f + e]);
+          }
+          v[e] = val * IO::round(glu_act<SINE, kSine>(g, round));
+        }
+        *reinterpret_cast<u32x2*>(orow + f) = u32x2{IO::pack2(v[0], v[1]), IO::pack2(v[2], v[3])};
+      }
+  }
+}
+
+}  // namespace proj_wide
 }  // namespace hb
 
 using namespace hb;
@@ -509,6 +716,132 @@ extern "C" int hb_proj(hipStream_t stream, const void* x, int dtype, int64_t x_r
     hipLaunchKernelGGL((proj::proj_gemm<Bf16Io, proj::kPlain, kProjWaves, kProjTokens>), dim3(grid),
                        dim3(64 * kProjWaves), 0, stream, a);
   return launched("proj");
+}
+
+extern "C" int hb_proj_glu(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const void* w,
+                           int64_t w_row_stride, const float* bias, int sinusoidal, void* out, int64_t out_row_stride,
+                           int64_t N, int K, int F) {
+  clear_error();
+  if (dtype != HB_BF16 && dtype != HB_F16)
+    return fail(HB_ERR_DTYPE, "the GLU projection takes HB_BF16 or HB_F16 (dtype %d)", dtype);
+  if (N < 1 || N > (1 << 24)) return fail(HB_ERR_SHAPE, "need 1 <= N <= 2^24 rows (N=%lld)", static_cast<long long>(N));
+  if (K < 64 || K % 64) return fail(HB_ERR_SHAPE, "the reduction length K=%d must be a positive multiple of 64", K);
+  if (F < 128 || F % 128 || F > (1 << 24))
+    return fail(HB_ERR_SHAPE, "the output width F=%d must be a positive multiple of 128", F);
+  int st = check_operand("x", x, N, x_row_stride, K);
+  if (st) return st;
+  st = check_operand("w", w, static_cast<int64_t>(2) * F, w_row_stride, K);
+  if (st) return st;
+  if (!out) return fail(HB_ERR_NULL, "out must be non-NULL");
+  if (reinterpret_cast<uintptr_t>(out) % 8 || out_row_stride < F || out_row_stride % 4)
+    return fail(HB_ERR_STRIDE, "out must be 8-byte aligned with a row stride >= F and a multiple of 4");
+  if ((st = check_extent("proj_glu", "out", N, out_row_stride, F))) return st;
+  {
+    const int64_t ob = rows_bytes(N, out_row_stride, F, 2);
+    if ((st = check_disjoint("proj_glu", "out", out, ob, "x", x, rows_bytes(N, x_row_stride, K, 2))) ||
+        (st = check_disjoint("proj_glu", "out", out, ob, "w", w, rows_bytes(2 * static_cast<int64_t>(F), w_row_stride,
+                                                                             K, 2))) ||
+        (st = check_disjoint("proj_glu", "out", out, ob, "bias", bias, static_cast<int64_t>(2) * F * 4)))
+      return st;
+  }
+  proj_wide::Args a{};
+  a.w = static_cast<const uint16_t*>(w);
+  a.x = static_cast<const uint16_t*>(x);
+  a.w_rs = w_row_stride;
+  a.x_rs = x_row_stride;
+  a.K = K;
+  a.N = static_cast<int>(N);
+  a.F = F;
+  a.nF = F / 128;
+  a.nT = static_cast<int>((N + proj_wide::TROWS - 1) / proj_wide::TROWS);
+  a.bias = bias;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_rs = out_row_stride;
+  const dim3 grid(static_cast<unsigned>(a.nF * a.nT)), block(256);
+  if (dtype == HB_F16) {
+    if (sinusoidal)
+      hipLaunchKernelGGL((proj_wide::proj_glu<F16Io, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((proj_wide::proj_glu<F16Io, false>), grid, block, 0, stream, a);
+  } else {
+    if (sinusoidal)
+      hipLaunchKernelGGL((proj_wide::proj_glu<Bf16Io, true>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((proj_wide::proj_glu<Bf16Io, false>), grid, block, 0, stream, a);
+  }
+  return launched("proj_glu");
+}
+
+extern "C" int hb_proj_residual(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const void* w,
+                                int64_t w_row_stride, const float* bias, const void* h, int64_t h_row_stride,
+                                const float* dyt, void* out_h, void* out_y, int64_t out_row_stride, int64_t N, int K,
+                                int F) {
+  clear_error();
+  if (dtype != HB_BF16 && dtype != HB_F16)
+    return fail(HB_ERR_DTYPE, "the residual projection takes HB_BF16 or HB_F16 (dtype %d)", dtype);
+  if (N < 1 || N > (1 << 24)) return fail(HB_ERR_SHAPE, "need 1 <= N <= 2^24 rows (N=%lld)", static_cast<long long>(N));
+  if (K < 64 || K % 64) return fail(HB_ERR_SHAPE, "the reduction length K=%d must be a positive multiple of 64", K);
+  if (F < 256 || F % 256 || F > (1 << 24))
+    return fail(HB_ERR_SHAPE, "the output width F=%d must be a positive multiple of 256", F);
+  int st = check_operand("x", x, N, x_row_stride, K);
+  if (st) return st;
+  st = check_operand("w", w, F, w_row_stride, K);
+  if (st) return st;
+  if (!h || !out_h) return fail(HB_ERR_NULL, "h and out_h must be non-NULL");
+  if (!dyt != !out_y) return fail(HB_ERR_NULL, "dyt and out_y are given together or not at all");
+  if (reinterpret_cast<uintptr_t>(h) % 8 || h_row_stride < F || h_row_stride % 4)
+    return fail(HB_ERR_STRIDE, "h must be 8-byte aligned with a row stride >= F and a multiple of 4");
+  if (reinterpret_cast<uintptr_t>(out_h) % 8 || (out_y && reinterpret_cast<uintptr_t>(out_y) % 8) ||
+      out_row_stride < F || out_row_stride % 4)
+    return fail(HB_ERR_STRIDE, "out_h and out_y must be 8-byte aligned with a row stride >= F and a multiple of 4");
+  if ((st = check_extent("proj_residual", "h", N, h_row_stride, F)) ||
+      (st = check_extent("proj_residual", "out", N, out_row_stride, F)))
+    return st;
+  {
+    const char* wn = "proj_residual";
+    const int64_t ob = rows_bytes(N, out_row_stride, F, 2), xb = rows_bytes(N, x_row_stride, K, 2);
+    const int64_t wb = rows_bytes(F, w_row_stride, K, 2), cb = static_cast<int64_t>(F) * 4;
+    if ((st = check_no_overlap(wn, "out_h", out_h, out_row_stride, F, "h", h, h_row_stride, F, N, 2, true)) ||
+        (st = check_no_overlap(wn, "out_y", out_y, out_row_stride, F, "h", h, h_row_stride, F, N, 2, false)) ||
+        (st = check_no_overlap(wn, "out_y", out_y, out_row_stride, F, "out_h", out_h, out_row_stride, F, N, 2,
+                               false)) ||
+        (st = check_disjoint(wn, "out_h", out_h, ob, "x", x, xb)) ||
+        (st = check_disjoint(wn, "out_h", out_h, ob, "w", w, wb)) ||
+        (st = check_disjoint(wn, "out_h", out_h, ob, "bias", bias, cb)) ||
+        (st = check_disjoint(wn, "out_h", out_h, ob, "dyt parameters", dyt, 2 * cb + 4)) ||
+        (st = check_disjoint(wn, "out_y", out_y, ob, "x", x, xb)) ||
+        (st = check_disjoint(wn, "out_y", out_y, ob, "w", w, wb)) ||
+        (st = check_disjoint(wn, "out_y", out_y, ob, "bias", bias, cb)) ||
+        (st = check_disjoint(wn, "out_y", out_y, ob, "dyt parameters", dyt, 2 * cb + 4)))
+      return st;
+  }
+  proj::Args a{};
+  a.w = static_cast<const uint16_t*>(w);
+  a.x = static_cast<const uint16_t*>(x);
+  a.w_rs = w_row_stride;
+  a.x_rs = x_row_stride;
+  a.K = K;
+  a.F = F;
+  a.B = 1;
+  a.L = static_cast<int>(N);
+  a.Lp = static_cast<int>(round_up(N, 128));
+  a.nF = F / proj::FT;
+  a.nT = static_cast<int>((a.Lp + kProjTokens - 1) / kProjTokens);
+  a.out = static_cast<uint16_t*>(out_h);
+  a.out_rs = out_row_stride;
+  a.res = static_cast<const uint16_t*>(h);
+  a.res_rs = h_row_stride;
+  a.bias = bias;
+  a.dyt = dyt;
+  a.out_y = static_cast<uint16_t*>(out_y);
+  const unsigned grid = static_cast<unsigned>(a.nF * a.nT);
+  if (dtype == HB_F16)
+    hipLaunchKernelGGL((proj::proj_gemm<F16Io, proj::kResidual, kProjWaves, kProjTokens>), dim3(grid),
+                       dim3(64 * kProjWaves), 0, stream, a);
+  else
+    hipLaunchKernelGGL((proj::proj_gemm<Bf16Io, proj::kResidual, kProjWaves, kProjTokens>), dim3(grid),
+                       dim3(64 * kProjWaves), 0, stream, a);
+  return launched("proj_residual");
 }
 
 // The attention over a projection: q and q_diff from rows [q | q_diff] (the qq buffer of hb_dit_qkv_proj) against

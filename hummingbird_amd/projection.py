@@ -1,5 +1,7 @@
-"""The DiT self-attention's projections on MI355X: `to_qkv` with the dense kernel's key preparation in its epilogue,
-and `to_out` (reference: sa3jax/dit.py:190 and 195, `_linear` without bias).
+"""The projections around the attention kernels on MI355X. The DiT self-attention's: `to_qkv` with the dense
+kernel's key preparation in its epilogue, and `to_out` (reference: sa3jax/dit.py:190 and 195, `_linear` without
+bias). The SAME-L block's: `glu_proj` with the GLU in its epilogue, and `to_out` / `proj_out` with the residual add
+and the next DyT in theirs (reference: sa3jax/same_l.py:161, 181-184, 191-192).
 
 `qkv_projection` runs `hb_dit_qkv_proj`: one matrix-core GEMM `h @ W_qkv^T` that never stores `qkv`; it writes the
 queries as rows `[q | q_diff]` and the prepared keys and values (RMSNorm, RoPE, value mask) into the attention
@@ -11,6 +13,8 @@ from __future__ import annotations
 import torch
 
 from hummingbird_amd import _lib
+from hummingbird_amd._derived import f32_vector
+from hummingbird_amd.band_attention import pack_dyt
 from hummingbird_amd.dense_attention import _f32, _require_gpu, dtype_code
 
 FUSED_DTYPES = (torch.bfloat16, torch.float16)
@@ -130,3 +134,75 @@ def linear(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     _lib.check(_lib.load().hb_proj(stream, x.data_ptr(), dtype_code(x.dtype), xs, w.data_ptr(), wstride, out.data_ptr(),
                                    f, n, k, f), "linear")
     return out
+
+
+def glu_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, sinusoidal: bool) -> torch.Tensor:
+    """`value * act(gate)` of `[value | gate] = x @ W^T (+ bias)` without storing the product (`hb_proj_glu`): the
+    SAME-L feed-forward's `glu_proj` and GLU (reference: same_l._feed_forward, same_l.py:181-183), with the cast
+    points of `elementwise.glu` on the rounded product. `weight` is the layer's `(2F, K)` (out x in), `bias` `(2F,)`
+    or None; act = sin(pi * gate) when `sinusoidal`, else SiLU. F a multiple of 128, K of 64."""
+    _require_gpu(x, "x")
+    if x.dtype not in FUSED_DTYPES:
+        raise TypeError(f"glu_linear takes bfloat16 or float16 inputs, got {x.dtype}")
+    w = weight.to(device=x.device, dtype=x.dtype)
+    n, xs = _rows(x, "x")
+    _, wstride = _rows(w, "weight")
+    f2, k = w.shape
+    if x.shape[-1] != k or f2 % 2:
+        raise ValueError(f"x has {x.shape[-1]} columns, weight is {tuple(w.shape)}")
+    f = f2 // 2
+    bias_p = 0
+    if bias is not None:
+        bias = f32_vector(bias, x.device)
+        if bias.numel() != f2:
+            raise ValueError(f"bias must have {f2} elements")
+        bias_p = bias.data_ptr()
+    out = torch.empty((*x.shape[:-1], f), dtype=x.dtype, device=x.device)
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    _lib.check(_lib.load().hb_proj_glu(stream, x.data_ptr(), dtype_code(x.dtype), xs, w.data_ptr(), wstride, bias_p,
+                                       int(bool(sinusoidal)), out.data_ptr(), f, n, k, f), "glu_linear")
+    return out
+
+
+def residual_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, h: torch.Tensor,
+                    norm: dict | None = None) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """`(h + (x @ W^T + bias), cast(DyT(...)))` with the residual add and the next DyT in the GEMM's epilogue
+    (`hb_proj_residual`): the SAME-L `to_out` / `proj_out` and the residual add after them (reference:
+    same_l._block, same_l.py:191-192, and same_l._linear), with the cast points of `elementwise.residual_dyt` on the
+    rounded product. `weight` is `(F, K)` (out x in), `bias` `(F,)` or None, `h` the residual `(..., F)`; without
+    `norm` (DyT params) the second result is None. F a multiple of 256, K of 64."""
+    _require_gpu(x, "x")
+    if x.dtype not in FUSED_DTYPES:
+        raise TypeError(f"residual_linear takes bfloat16 or float16 inputs, got {x.dtype}")
+    w = weight.to(device=x.device, dtype=x.dtype)
+    n, xs = _rows(x, "x")
+    _, wstride = _rows(w, "weight")
+    f, k = w.shape
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} columns, weight {k}")
+    if h.shape[:-1] != x.shape[:-1] or h.shape[-1] != f or h.dtype != x.dtype:
+        raise ValueError(f"h must be {(*x.shape[:-1], f)} of {x.dtype}, got {tuple(h.shape)} {h.dtype}")
+    _, hs = _rows(h, "h")
+    bias_p = 0
+    if bias is not None:
+        bias = f32_vector(bias, x.device)
+        if bias.numel() != f:
+            raise ValueError(f"bias must have {f} elements")
+        bias_p = bias.data_ptr()
+    params = pack_dyt(norm, f, x.device) if norm is not None else None
+    out_h = torch.empty(h.shape, dtype=x.dtype, device=x.device)
+    out_y = torch.empty(h.shape, dtype=x.dtype, device=x.device) if norm is not None else None
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    _lib.check(_lib.load().hb_proj_residual(stream, x.data_ptr(), dtype_code(x.dtype), xs, w.data_ptr(), wstride,
+                                            bias_p, h.data_ptr(), hs, params.data_ptr() if params is not None else 0,
+                                            out_h.data_ptr(), out_y.data_ptr() if out_y is not None else 0, f, n, k,
+                                            f), "residual_linear")
+    return out_h, out_y
+
+
+def same_l_supported(dtype: torch.dtype, dim: int, ff_inner: int, qkv_width: int) -> bool:
+    """Whether the SAME-L block's projections take the fused kernels: bf16 or half, model width a multiple of 256,
+    feed-forward width a multiple of 256 (its GLU half of 128 and proj_out's reduction of 64), the to_qkv width a
+    multiple of 256."""
+    return (dtype in FUSED_DTYPES and dim % 256 == 0 and ff_inner % 256 == 0 and qkv_width % 256 == 0 and dim > 0
+            and ff_inner > 0)

@@ -157,6 +157,28 @@ int hb_dense_attend_qq(hipStream_t stream, const void* qq, int dtype, int64_t ro
 int hb_proj(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const void* w, int64_t w_row_stride,
             void* out, int64_t out_row_stride, int64_t N, int K, int F);
 
+/* ---- SAME-L decoder block: projections with the work next to them in their epilogues ----------------------
+ * hb_proj_glu replaces the feed-forward's `glu_proj` and the GLU after it (same_l._feed_forward,
+ *   sa3jax/same_l.py:181-183): out (N, F) = value * act(gate) for [value | gate] = x (N, K) x W^T (K, 2F), W (2F, K)
+ *   the layer's weight as stored (out x in; value rows first). The product is rounded to dtype (the reference's
+ *   stored glu_proj output), `bias` (2F floats holding values of dtype, or NULL) added and rounded, then act and the
+ *   product with hb_glu's cast points (act = SiLU, or sin(pi * gate) when `sinusoidal` != 0); the 2F-wide product is
+ *   never stored. K a multiple of 64, F of 128; dtype HB_BF16 or HB_F16.
+ * hb_proj_residual replaces `to_out` / `proj_out` and the residual add after them (sa3jax/same_l.py:161, 184 with
+ *   191, 192): out_h (N, F) = h + (x W^T + bias) and, with `dyt` (packed as for hb_dyt), out_y = cast(DyT(out_h)),
+ *   the next GEMM's input; the product, the bias add and the sum are each rounded to dtype, as hb_residual_dyt
+ *   computes them from the stored product. W (F, K); K a multiple of 64, F of 256; bias: F floats or NULL; `dyt`
+ *   and `out_y` both given or both NULL. out_h may be h itself (same row stride); otherwise no output shares an
+ *   element with h, x, w, bias, dyt or the other output (HB_ERR_STRIDE).
+ * Both: x rows with stride x_row_stride (>= K, a multiple of 8), x and w 16-byte aligned, outputs 8-byte aligned
+ *   with row strides >= F and multiples of 4; fp32 accumulation over K in order. */
+int hb_proj_glu(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const void* w,
+                int64_t w_row_stride, const float* bias, int sinusoidal, void* out, int64_t out_row_stride, int64_t N,
+                int K, int F);
+int hb_proj_residual(hipStream_t stream, const void* x, int dtype, int64_t x_row_stride, const void* w,
+                     int64_t w_row_stride, const float* bias, const void* h, int64_t h_row_stride, const float* dyt,
+                     void* out_h, void* out_y, int64_t out_row_stride, int64_t N, int K, int F);
+
 /* ---- SAME-L band differential attention -----------------------------------------------------------------
  * Replaces band_attention.band_attention (sa3jax/band_attention.py:123-180) and the XLA chain it stands in
  * for (sa3jax/same_l.py:151-169). Per (batch b, head h):

@@ -240,6 +240,44 @@ def test_projection_entry_points_reject_before_any_launch(lib):
     assert attend(rs=2 * H * D - 8) == 7 and attend(dtype=1) == 3 and attend(wsb=need - 1) == 8
 
 
+def test_same_l_projection_entry_points_reject_before_any_launch(lib):
+    """hb_proj_glu and hb_proj_residual validate dtype, shapes, strides, alignment, the dyt / out_y pairing and which
+    buffers may alias on the host (fake, never dereferenced addresses; no kernel is launched)."""
+    x, w, o, h, y, v = 0x100000, 0x400000, 0x800000, 0xC00000, 0x1000000, 0x1400000
+
+    def glu(**kw):
+        a = dict(x=x, dtype=0, xs=128, w=w, ws=128, bias=None, sine=1, out=o, os=256, N=10, K=128, F=256)
+        a.update(kw)
+        return lib.hb_proj_glu(None, a["x"], a["dtype"], a["xs"], a["w"], a["ws"], a["bias"], a["sine"], a["out"],
+                               a["os"], a["N"], a["K"], a["F"])
+    assert glu(dtype=1) == 3 and glu(dtype=5) == 3       # fp32 is not taken by the fused GEMMs
+    assert glu(F=200) == 2 and glu(F=64) == 2 and glu(K=100) == 2 and glu(K=0) == 2 and glu(N=0) == 2
+    assert glu(N=(1 << 24) + 1) == 2
+    assert glu(x=None) == 1 and glu(w=None) == 1 and glu(out=None) == 1
+    assert glu(xs=120) == 7 and glu(x=x + 8) == 7 and glu(ws=100) == 7  # strides and alignment of the operands
+    assert glu(os=200) == 7 and glu(out=o + 4) == 7                     # out row stride below F, misaligned out
+    assert glu(out=x) == 7 and glu(out=w + 512) == 7                    # out over x, over W (2F rows of it)
+    assert glu(out=w + 2 * 256 * 128 * 2 - 16) == 7                    # the last 16 bytes of W
+    assert glu(bias=o + 64) == 7                                        # the bias (2F floats) inside out
+
+    def res(**kw):
+        a = dict(x=x, dtype=0, xs=128, w=w, ws=128, bias=None, h=h, hs=256, dyt=None, oh=o, oy=None, os=256, N=10,
+                 K=128, F=256)
+        a.update(kw)
+        return lib.hb_proj_residual(None, a["x"], a["dtype"], a["xs"], a["w"], a["ws"], a["bias"], a["h"], a["hs"],
+                                    a["dyt"], a["oh"], a["oy"], a["os"], a["N"], a["K"], a["F"])
+    assert res(dtype=1) == 3
+    assert res(F=128) == 2 and res(K=96) == 2 and res(N=0) == 2
+    assert res(h=None) == 1 and res(oh=None) == 1 and res(x=None) == 1
+    assert res(dyt=v) == 1 and res(oy=y) == 1                             # dyt and out_y come together
+    assert res(hs=200) == 7 and res(h=h + 4) == 7 and res(os=128) == 7    # strides and alignment
+    assert res(oh=x) == 7 and res(oh=w) == 7                              # out_h over the GEMM operands
+    assert res(oh=h, os=512) == 7                                         # h itself under another row stride
+    assert res(oh=h + 8) == 7                                             # partly over h
+    assert res(dyt=v, oy=h) == 7 and res(dyt=v, oy=o) == 7 and res(dyt=v, oy=x) == 7
+    assert res(dyt=o + 64, oy=y) == 7 and res(bias=o + 64) == 7           # the vectors inside an output
+
+
 def test_dit_block_entry_points_reject_before_any_launch(lib):
     """hb_rms_modulate and hb_gated_residual validate dtype, shapes, strides, alignment and their optional
     operands on the host (fake, never dereferenced addresses)."""

@@ -121,6 +121,36 @@ def test_glu_sine_large_gates_vs_oracle(scale):
     assert_within_one_bf16_step(got, ref, f"glu sine x{scale}", max_frac=0.02)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_glu_sine_every_gate_vs_oracle(dtype):
+    """Every finite gate value of the dtype (value 1, so the output is the rounded activation) through the sine GLU
+    against the oracle's float64 sine: the kernel's argument reductions (Cody-Waite and the hardware sine for bf16,
+    with the exact table reduction once |pi g| > 2^16; the three-term split and the polynomial for half) on every
+    input they can receive. Gates whose product pi g overflows give NaN on both sides."""
+    announce(f"glu sine every {dtype} gate")
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    bits = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    gates = bits.view(tdt).float()
+    gates = gates[torch.isfinite(gates)]
+    f = 256
+    rows = -(-gates.numel() // f)
+    g = torch.zeros(rows * f)
+    g[: gates.numel()] = gates
+    proj = torch.cat([torch.ones(rows, f), g.reshape(rows, f)], dim=1).to(DEV, tdt)
+    got = elementwise.glu(proj, True).float().cpu().numpy()
+    with np.errstate(invalid="ignore"):
+        ref = oblock.glu(proj.float().cpu().numpy(), True, dtype)
+    nan_g, nan_r = np.isnan(got), np.isnan(ref)
+    assert (nan_g == nan_r).all(), f"NaN at {int((nan_g != nan_r).sum())} positions that differ"
+    keep = ~nan_r
+    got, ref = got[keep], ref[keep]
+    bits_ = 8 if dtype == "bf16" else 11
+    step = np.ldexp(1.0, np.frexp(np.maximum(np.abs(ref), 2.0 ** -126))[1] - bits_)
+    diff = np.abs(got.astype(np.float64) - ref)
+    assert (diff <= step).all(), f"{int((diff > step).sum())} activations more than one step from the oracle"
+    assert (diff == 0).mean() >= 0.999, f"only {(diff == 0).mean():.5f} of the activations equal the oracle's"
+
+
 def test_elementwise_padded_rows():
     """Column slices of wider tensors (row stride > width) give the same values as contiguous inputs."""
     announce("dyt / glu padded rows")
