@@ -266,6 +266,23 @@ def test_band_multistep_runs_vs_torch_chain(shape):
     check_vs_torch_chain(b, s, h, 64, w, half, gm, f"multistep {shape}")
 
 
+# At least 16 steps per CU, with a (batch, head) count that does not divide the CU count: the ring kernel then
+# splits the steps weighted by ring fills, so the workgroups that cross a (batch, head) boundary get fewer steps.
+FILL_WEIGHTED = [  # (B, S, H, window, half, gamma_mean)
+    (1, 23086, 24, 17, 16, 1.0),  # the reference decoder geometry
+    (1, 50000, 6, 40, 32, 1.0),
+    (2, 30000, 5, 128, 32, 1.0),
+]
+
+
+@pytest.mark.parametrize("shape", FILL_WEIGHTED, ids=lambda s: "B%dS%dH%dw%dh%dg%g" % s)
+def test_band_fill_weighted_split_vs_torch_chain(shape):
+    b, s, h, w, half, gm = shape
+    announce(f"band bf16 fill-weighted split {shape}")
+    assert torch.cuda.get_device_properties(0).multi_processor_count % (b * h) != 0
+    check_vs_torch_chain(b, s, h, 64, w, half, gm, f"fill-weighted {shape}")
+
+
 # Windows at the edges of the ring kernel's interior-step patterns. For w in (64 (C - 1), 64 C] an interior
 # step's attention wave attends the 32-key halves t = -T .. T around its own queries, T = floor((w + 31) / 32), and
 # masks those with |t| >= M = floor((w + 1) / 32); the pattern changes at w = 64 C - 33, 64 C - 31 and 64 C - 1.
