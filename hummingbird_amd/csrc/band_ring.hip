@@ -37,8 +37,9 @@
 // (ds_read_b128, 8 or 16 rows per cycle), the transposing V reads (ds_read_b64_tr_b16, 4 rows x 32 B per 16
 // lanes) and the Q reads hit distinct banks.
 //
-// The runs are the flattened (batch, head, step) range split evenly over one workgroup per CU; consecutive
-// workgroups go to different XCDs, so the same run position of every head (the same RoPE rows) shares an L2.
+// The runs are the flattened (batch, head, step) range split over one workgroup per CU, evenly, or weighted by
+// ring fills where (batch, head) boundaries fall inside workgroups (Range); consecutive workgroups go to
+// different XCDs, so the same run position of every head (the same RoPE rows) shares an L2.
 #include <type_traits>
 
 #include "api.h"
