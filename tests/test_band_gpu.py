@@ -272,6 +272,7 @@ FILL_WEIGHTED = [  # (B, S, H, window, half, gamma_mean)
     (1, 23086, 24, 17, 16, 1.0),  # the reference decoder geometry
     (1, 50000, 6, 40, 32, 1.0),
     (2, 30000, 5, 128, 32, 1.0),
+    (1, 90000, 3, 0, 32, 1.0),    # w = 0: the diagonal half only
 ]
 
 
