@@ -35,7 +35,7 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
 # (written by hummingbird_amd.rocprof_summary); reported as roofline.traffic when present.
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_120s_clip.json"
 # Kernels that the two calls launch at these shapes (D = 64; window 128 takes the two-tile ring variant).
-DENSE_KERNEL = "dense_attend_bf16<64,128>"
+DENSE_KERNEL = "dense_attend_bf16<64,128,4>"
 BAND_KERNEL = "band_ring_bf16<2>"
 
 
@@ -443,9 +443,12 @@ def decoder_gemms(x, p, cfg, stream) -> dict:
 def decoder_shape(dev, gen) -> dict:
     """The SAME-L decoder's 12 blocks for a 120 s clip at the reference's medium geometry (1358 latents x 17 = 23086
     frames, dim 1536 = 24 heads of 64, ff 4608, half-width 17, the last 8 blocks with the sine gate; random weights,
-    bf16): ms per clip for the chained loop (`same_l.blocks`, each block handing the next its pre_norm DyT) and for
-    the block-by-block loop, medians of 7 interleaved runs after one warm-up each. The reference's published figure for its whole decode (these blocks plus the
-    bottleneck, token interleave and output mapping) is 61 ms on a TPU v6e-1."""
+    bf16): ms per clip for the chained loop (`same_l.blocks`, each block handing the next its pre_norm DyT), for the
+    block-by-block loop and for the chained loop on this package's projection GEMMs with fused epilogues
+    (projections="hip"), medians of 7 interleaved runs after one warm-up each; then each projection of one block
+    timed alone, fused against hipBLASLt plus the elementwise kernel (`decoder_gemms`). The reference's published
+    figure for its whole decode (these blocks plus the bottleneck, token interleave and output mapping) is 61 ms on
+    a TPU v6e-1."""
     import torch
 
     from hummingbird_amd import same_l
