@@ -9,7 +9,8 @@ buffers. Inputs follow the seeded recipe of `hummingbird_amd.workloads` (synthet
 The JSON line also carries, for the dominant kernel (dense attention), a roofline object computed from its
 average launch duration measured here with HIP events on its own stream, and the same for the band kernel
 (`roofline_band`); plus the CPU baseline: the NumPy restatement of the reference XLA chains (the oracle, fp32
-accumulation) timed on a bounded sample on this host and scaled to one clip.
+accumulation) timed on this host on whole config-0, config-1 and config-2 calls, the clip composed from the
+per-call times.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
